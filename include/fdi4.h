@@ -1,0 +1,180 @@
+/*
+ * fdi4 -- C ABI of the MI355X (gfx950) INT4 key quantizer and fused INT4
+ * flash-decoding kernels.
+ *
+ * Every entry point is a plain C function over device pointers, sizes and
+ * strides, enqueued asynchronously on the given HIP stream (0 = the null
+ * stream); none synchronizes the host. Return value: a hipError_t code
+ * (0 = hipSuccess, 1 = hipErrorInvalidValue for rejected sizes, otherwise the
+ * launch error). Inputs are borrowed for the duration of the enqueued work;
+ * nothing is retained between calls.
+ *
+ * The library is libfdi4.so in the package directory
+ * int4-kv-cache-quantization-cuda-triton-pallas_amd/flash_decode_int4/.
+ */
+#ifndef FDI4_H_
+#define FDI4_H_
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FDI4_ABI_VERSION 1
+
+enum fdi4_value_dtype { FDI4_V_F32 = 0, FDI4_V_F16 = 1 };
+
+/* Device layout of a paged INT4 key/value cache.
+ *
+ *   k_pages   packed keys, byte j of a row = channel 2j (low nibble) |
+ *             channel 2j+1 (high nibble); address of row r of physical page p,
+ *             kv-head h: k_pages + p*k_page_stride + h*k_head_stride +
+ *             r*k_row_stride (bytes). A row holds head_dim/2 bytes.
+ *   v_pages   values (fp32 or fp16), same addressing in elements.
+ *   k_scale,  per-channel scale and zero-point of the scale group of logical
+ *   k_zp      page lp of sequence b: element offset
+ *             b*s_batch_stride + h*s_head_stride + (lp/pages_per_group)*s_group_stride
+ *             + p*s_page_stride (+ channel). s_page_stride != 0 (scales attached to
+ *             physical pages) requires pages_per_group == 1.
+ *   page_table [B, pt_batch_stride] int32 physical page of each logical page;
+ *             NULL means logical page == physical page. Entries are clamped to
+ *             [0, num_pages) on the device, so a bad table cannot address
+ *             memory outside the pool (the results are then meaningless).
+ *   seq_lens  [B] int32 valid tokens; NULL means every sequence spans max_pages
+ *             full pages (then page_lens gives the valid rows).
+ *   page_lens [B, pl_batch_stride] int32 valid rows of each logical page, or NULL;
+ *             values are clamped to [0, page_rows].
+ * head_dim is 64, 128 or 256 for the paged entry points. page_rows and
+ * pages_per_group are >= 1. Strides of 0 share one stream between sequences or
+ * heads (the reference's shared-page-stream semantics).
+ */
+typedef struct fdi4_paged_cache {
+  uint8_t* k_pages;
+  int64_t k_page_stride, k_head_stride, k_row_stride;
+  void* v_pages;
+  int32_t v_dtype;
+  int64_t v_page_stride, v_head_stride, v_row_stride;
+  float* k_scale;
+  float* k_zp;
+  int64_t s_batch_stride, s_head_stride, s_group_stride, s_page_stride;
+  const int32_t* page_table;
+  int64_t pt_batch_stride;
+  const int32_t* seq_lens;
+  const int32_t* page_lens;
+  int64_t pl_batch_stride;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t page_rows;
+  int32_t pages_per_group;
+  int32_t max_pages;  /* logical pages per sequence (columns of page_table) */
+  int32_t num_pages;  /* physical pages in the pool */
+} fdi4_paged_cache;
+
+/* ABI version of the loaded library (FDI4_ABI_VERSION). */
+int fdi4_abi_version(void);
+
+/* Human-readable text of a status code returned by this library. */
+const char* fdi4_error_string(int status);
+
+/* Per-channel asymmetric INT4 quantization of kv[num_rows, num_channels]
+ * (row-major, contiguous) as ONE scale group over all rows; q_out is one
+ * value per byte [num_rows, num_channels], scale_out/zp_out are [num_channels].
+ * Bit-exact with NumPy: round half to even, IEEE float32 division.
+ * Replaces cu_quantize_int4 (reference csrc/flash_decode_int4.cu:228-247,
+ * declared at csrc/bindings.cpp:17-18); same arguments. Takes a stream-ordered
+ * temporary from hipMallocAsync for the row-tile partials. */
+int fdi4_quantize_int4(const float* kv, int num_rows, int num_channels, uint8_t* q_out,
+                       float* scale_out, float* zp_out, hipStream_t stream);
+
+/* Workspace needed by fdi4_quantize_rows. */
+size_t fdi4_quantize_rows_workspace_bytes(int64_t num_rows, int num_channels);
+
+/* General form of fdi4_quantize_int4 with row strides (elements / bytes),
+ * nibble-packed output when packed != 0 (q_out row = ceil(C/2) bytes), and a
+ * caller-provided workspace (no allocation). Serves the reference's
+ * ops.quantize_int4 (src/ops.py:111-161) and the paged cache's block writes
+ * (src/vllm_integration.py:48-56). */
+int fdi4_quantize_rows(const float* kv, int64_t num_rows, int num_channels,
+                       int64_t kv_row_stride, uint8_t* q_out, int64_t q_row_stride, int packed,
+                       float* scale_out, float* zp_out, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+/* Grouped quantization of keys k[b, h, t, :] (element strides, channel stride
+ * 1, 16-byte aligned rows) for t < cache->seq_lens[b]: every group_rows tokens
+ * of one (sequence, kv-head) form one scale group (a partial last group uses
+ * its valid rows only); packed rows are written through cache->page_table
+ * and the group scales to cache->k_scale / k_zp. group_rows is 64, 128 or 256
+ * and a multiple of cache->page_rows; head_dim is 64, 128 or 256. Counterpart
+ * of the reference's per-group quantize_int4_ref + pack_int4
+ * (src/quantize_int4_ref.py:23-84, src/int4_pack.py:14-29) on device. */
+int fdi4_quantize_paged(const float* k, int batch, int max_tokens, int64_t k_batch_stride,
+                        int64_t k_head_stride, int64_t k_row_stride, int group_rows,
+                        const fdi4_paged_cache* cache, hipStream_t stream);
+
+/* Fused INT4 flash decoding with the reference's exact arguments: query
+ * [B, H, D], k_q [nb, bs, D] one INT4 value per byte, k_scale/k_zp [nb, D],
+ * value [nb, bs, D] fp32, block_lens [nb]; every (b, h) query attends the same
+ * page stream; 1 <= D <= 256. Replaces cu_flash_decode_int4 (reference
+ * csrc/flash_decode_int4.cu:249-284, declared at csrc/bindings.cpp:19-21).
+ * Packs keys into a stream-ordered temporary from hipMallocAsync, then runs
+ * the split-K decode. */
+int fdi4_flash_decode_int4(const float* query, const uint8_t* k_q, const float* k_scale,
+                           const float* k_zp, const float* value, const int* block_lens,
+                           int batch_size, int num_heads, int head_dim, int num_blocks,
+                           int block_size, float* output, hipStream_t stream);
+
+/* Workspace for fdi4_flash_decode_int4_ws. */
+size_t fdi4_flash_decode_int4_workspace_bytes(int batch_size, int num_heads, int head_dim,
+                                              int num_blocks, int block_size);
+
+/* fdi4_flash_decode_int4 with a caller-provided workspace (no allocation);
+ * serves the reference's _C.flash_decode_int4 binding (csrc/bindings.cpp:56-127). */
+int fdi4_flash_decode_int4_ws(const float* query, const uint8_t* k_q, const float* k_scale,
+                              const float* k_zp, const float* value, const int* block_lens,
+                              int batch_size, int num_heads, int head_dim, int num_blocks,
+                              int block_size, float* output, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
+/* Split count the decode would choose for this shape when num_splits <= 0. */
+int fdi4_decode_num_splits(int batch, int num_q_heads, const fdi4_paged_cache* cache);
+
+/* Workspace for fdi4_decode_paged with the given split count (0 when 1). */
+size_t fdi4_decode_workspace_bytes(int batch, int num_q_heads, int head_dim, int num_splits);
+
+/* Split-K paged decode: out[b, h, :] = softmax(q[b,h].K^T) V over the valid
+ * rows of sequence b, kv-head h / (num_q_heads / num_kv_heads); unscaled
+ * logits; empty pages skipped; a sequence with no valid row gives exact
+ * zeros. num_splits <= 0 selects fdi4_decode_num_splits. With more than one
+ * split the partials go to the workspace and the merge kernel runs on the
+ * same stream. Counterpart of the reference's flash_decode_int4_kernel
+ * (csrc/flash_decode_int4.cu:104-221) generalized to per-sequence page
+ * tables, group scales and packed keys. */
+int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_batch_stride,
+                      int64_t q_head_stride, const fdi4_paged_cache* cache, float* out,
+                      int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Log-sum-exp merge of split partials part_acc [B, Hq, S, D] fp32 and
+ * part_ml [B, Hq, S, 2] fp64 (m, l), as written by fdi4_decode_paged, into
+ * out. Exposed so that partials gathered from several devices can be merged.
+ * Counterpart of the cross-warp merge of the reference kernel
+ * (csrc/flash_decode_int4.cu:186-220). */
+int fdi4_merge_splits(const float* part_acc, const double* part_ml, int batch, int num_q_heads,
+                      int head_dim, int num_splits, float* out, int64_t out_batch_stride,
+                      int64_t out_head_stride, hipStream_t stream);
+
+/* Device nibble packing: out[r, j] = q[r, 2j] | q[r, 2j+1] << 4 for
+ * j < ceil(C/2) (odd C zero-padded), zero for ceil(C/2) <= j < out_cols.
+ * Values are taken modulo 16. Counterpart of pack_int4 (reference
+ * src/int4_pack.py:14-29). */
+int fdi4_pack_int4(const uint8_t* q, int64_t rows, int num_channels, int64_t q_row_stride,
+                   uint8_t* out, int64_t out_row_stride, int out_cols, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FDI4_H_ */

@@ -1,0 +1,463 @@
+// extern "C" entry points of libfdi4 (declared in include/fdi4.h).
+//
+// Host-side only: argument validation (every size and alignment the kernels
+// assume is checked here, so a malformed call becomes hipErrorInvalidValue
+// instead of an out-of-bounds device access), translation of the public
+// layout into kernel argument blocks, split-count selection and workspace
+// carving.
+
+#include <limits.h>
+
+#include <algorithm>
+
+#include "../../include/fdi4.h"
+#include "fdi4_internal.hpp"
+
+namespace {
+
+using fdi4::DecodeArgs;
+using fdi4::QuantPagedArgs;
+
+constexpr int kWaves = 4;          // waves per decode workgroup
+constexpr int kTargetWgs = 2048;   // decode workgroups aimed for (8 per CU on 256 CUs)
+constexpr int kMinChunksPerWave = 2;
+constexpr size_t kAlign = 256;
+
+inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+bool valid_head_dim(int d) { return d == 64 || d == 128 || d == 256; }
+
+int padded_head_dim(int d) { return d <= 64 ? 64 : (d <= 128 ? 128 : 256); }
+
+int chunks_per_seq(const fdi4_paged_cache* c) {
+  return c->max_pages * ceil_div(c->page_rows, 16);
+}
+
+int auto_splits(int batch, int hq, int chunks) {
+  if (chunks <= 0) return 1;
+  const int64_t bh = (int64_t)batch * hq;
+  int s = (int)((kTargetWgs + bh - 1) / bh);
+  const int smax = std::max(1, chunks / (kWaves * kMinChunksPerWave));
+  return std::max(1, std::min(s, smax));
+}
+
+size_t decode_ws_bytes(int batch, int hq, int d, int splits) {
+  if (splits <= 0) return 0;
+  const size_t n = (size_t)batch * hq * splits;
+  return align_up(n * d * sizeof(float)) + align_up(n * 2 * sizeof(double));
+}
+
+int check_cache(const fdi4_paged_cache* c, bool need_values) {
+  if (!c || !c->k_pages || !c->k_scale || !c->k_zp) return hipErrorInvalidValue;
+  if (!valid_head_dim(c->head_dim)) return hipErrorInvalidValue;
+  if (c->num_kv_heads < 1 || c->page_rows < 1 || c->pages_per_group < 1 || c->max_pages < 0 ||
+      c->num_pages < 1)
+    return hipErrorInvalidValue;
+  if (c->s_page_stride != 0 && c->pages_per_group != 1) return hipErrorInvalidValue;
+  const int kbl = c->head_dim == 64 ? 8 : 16;  // bytes a lane loads from a key row
+  if (!aligned(c->k_pages, kbl) || c->k_page_stride % kbl || c->k_head_stride % kbl ||
+      c->k_row_stride % kbl || c->k_row_stride < c->head_dim / 2)
+    return hipErrorInvalidValue;
+  if (!aligned(c->k_scale, 16) || !aligned(c->k_zp, 16) || c->s_batch_stride % 4 ||
+      c->s_head_stride % 4 || c->s_group_stride % 4 || c->s_page_stride % 4)
+    return hipErrorInvalidValue;
+  if (need_values) {
+    if (!c->v_pages || (c->v_dtype != FDI4_V_F32 && c->v_dtype != FDI4_V_F16))
+      return hipErrorInvalidValue;
+    const int veb = c->v_dtype == FDI4_V_F32 ? 4 : 2;
+    if (!aligned(c->v_pages, 16) || (c->v_page_stride * veb) % 16 ||
+        (c->v_head_stride * veb) % 16 || (c->v_row_stride * veb) % 16 ||
+        c->v_row_stride < c->head_dim)
+      return hipErrorInvalidValue;
+  }
+  return hipSuccess;
+}
+
+void set_pool_threshold(hipStream_t) {
+  static bool done = false;
+  if (done) return;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  hipMemPool_t pool;
+  if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+    uint64_t keep = UINT64_MAX;
+    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+  }
+  done = true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fdi4_abi_version(void) { return FDI4_ABI_VERSION; }
+
+const char* fdi4_error_string(int status) { return hipGetErrorString((hipError_t)status); }
+
+size_t fdi4_quantize_rows_workspace_bytes(int64_t num_rows, int num_channels) {
+  if (num_rows <= 0 || num_channels <= 0) return 0;
+  return fdi4::rows_workspace_bytes(num_rows, num_channels);
+}
+
+int fdi4_quantize_rows(const float* kv, int64_t num_rows, int num_channels, int64_t kv_row_stride,
+                       uint8_t* q_out, int64_t q_row_stride, int packed, float* scale_out,
+                       float* zp_out, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
+  if (!kv || !q_out || !scale_out || !zp_out) return hipErrorInvalidValue;
+  if (num_rows <= 0 || num_channels <= 0) return hipErrorInvalidValue;
+  if ((num_rows + 255) / 256 > 65535) return hipErrorInvalidValue;  // grid.y of the row tiles
+  const int qcols = packed ? (num_channels + 1) / 2 : num_channels;
+  if (kv_row_stride < num_channels || q_row_stride < qcols) return hipErrorInvalidValue;
+  if (!workspace || !aligned(workspace, 8) ||
+      workspace_bytes < fdi4::rows_workspace_bytes(num_rows, num_channels))
+    return hipErrorInvalidValue;
+  return fdi4::launch_quantize_rows(kv, num_rows, num_channels, kv_row_stride, q_out,
+                                    q_row_stride, packed != 0, scale_out, zp_out, workspace,
+                                    stream);
+}
+
+int fdi4_quantize_int4(const float* kv, int num_rows, int num_channels, uint8_t* q_out,
+                       float* scale_out, float* zp_out, hipStream_t stream) {
+  if (num_rows <= 0 || num_channels <= 0 || !kv || !q_out || !scale_out || !zp_out)
+    return hipErrorInvalidValue;
+  const size_t wsb = fdi4::rows_workspace_bytes(num_rows, num_channels);
+  set_pool_threshold(stream);
+  void* ws = nullptr;
+  hipError_t e = hipMallocAsync(&ws, wsb, stream);
+  if (e != hipSuccess) return e;
+  int rc = fdi4_quantize_rows(kv, num_rows, num_channels, num_channels, q_out, num_channels, 0,
+                              scale_out, zp_out, ws, wsb, stream);
+  hipError_t f = hipFreeAsync(ws, stream);
+  return rc != hipSuccess ? rc : f;
+}
+
+int fdi4_quantize_paged(const float* k, int batch, int max_tokens, int64_t k_batch_stride,
+                        int64_t k_head_stride, int64_t k_row_stride, int group_rows,
+                        const fdi4_paged_cache* cache, hipStream_t stream) {
+  int rc = check_cache(cache, false);
+  if (rc != hipSuccess) return rc;
+  if (!k || !cache->seq_lens || !cache->page_table) return hipErrorInvalidValue;
+  if (batch < 0 || max_tokens < 0 || batch > 65535 || cache->num_kv_heads > 65535)
+    return hipErrorInvalidValue;
+  if (group_rows != 64 && group_rows != 128 && group_rows != 256) return hipErrorInvalidValue;
+  if (group_rows % cache->page_rows) return hipErrorInvalidValue;
+  if (cache->pages_per_group != group_rows / cache->page_rows || cache->s_page_stride != 0)
+    return hipErrorInvalidValue;
+  if ((int64_t)cache->max_pages * cache->page_rows < max_tokens) return hipErrorInvalidValue;
+  // 16-byte row loads of the keys and 16-byte stores of packed rows.
+  if (!aligned(k, 16) || k_batch_stride % 4 || k_head_stride % 4 || k_row_stride % 4 ||
+      k_row_stride < cache->head_dim)
+    return hipErrorInvalidValue;
+  if (cache->k_page_stride % 16 || cache->k_head_stride % 16 || cache->k_row_stride % 16 ||
+      !aligned(cache->k_pages, 16))
+    return hipErrorInvalidValue;
+  QuantPagedArgs a;
+  a.k = k;
+  a.k_b = k_batch_stride;
+  a.k_h = k_head_stride;
+  a.k_t = k_row_stride;
+  a.seq_lens = cache->seq_lens;
+  a.page_table = cache->page_table;
+  a.pt_b = cache->pt_batch_stride;
+  a.k_pages = cache->k_pages;
+  a.kp_page = cache->k_page_stride;
+  a.kp_head = cache->k_head_stride;
+  a.kp_row = cache->k_row_stride;
+  a.scale = cache->k_scale;
+  a.zp = cache->k_zp;
+  a.s_b = cache->s_batch_stride;
+  a.s_h = cache->s_head_stride;
+  a.s_g = cache->s_group_stride;
+  a.page_rows = cache->page_rows;
+  a.num_pages = cache->num_pages;
+  a.max_tokens = max_tokens;
+  return fdi4::launch_quantize_paged(a, cache->head_dim, group_rows, batch, cache->num_kv_heads,
+                                     max_tokens, stream);
+}
+
+int fdi4_decode_num_splits(int batch, int num_q_heads, const fdi4_paged_cache* cache) {
+  if (!cache || batch <= 0 || num_q_heads <= 0 || cache->page_rows < 1) return 1;
+  return auto_splits(batch, num_q_heads, chunks_per_seq(cache));
+}
+
+size_t fdi4_decode_workspace_bytes(int batch, int num_q_heads, int head_dim, int num_splits) {
+  if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0 || num_splits <= 1) return 0;
+  return decode_ws_bytes(batch, num_q_heads, head_dim, num_splits);
+}
+
+size_t fdi4_decode_partials_bytes(int batch, int num_q_heads, int head_dim, int num_splits) {
+  if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0 || num_splits <= 0) return 0;
+  return decode_ws_bytes(batch, num_q_heads, head_dim, num_splits);
+}
+
+int fdi4_merge_splits(const float* part_acc, const double* part_ml, int batch, int num_q_heads,
+                      int head_dim, int num_splits, float* out, int64_t out_batch_stride,
+                      int64_t out_head_stride, hipStream_t stream) {
+  if (!part_acc || !part_ml || !out || batch <= 0 || num_q_heads <= 0 || num_splits <= 0)
+    return hipErrorInvalidValue;
+  if (!valid_head_dim(head_dim) || batch > 65535 || num_q_heads > 65535)
+    return hipErrorInvalidValue;
+  return fdi4::launch_merge(part_acc, part_ml, batch, num_q_heads, head_dim, num_splits, out,
+                            out_batch_stride, out_head_stride, stream);
+}
+
+namespace {
+
+// Validate and fill the kernel argument block shared by the decode entry points.
+int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_batch_stride,
+                     int64_t q_head_stride, const fdi4_paged_cache* cache, int num_splits,
+                     DecodeArgs* a) {
+  int rc = check_cache(cache, true);
+  if (rc != hipSuccess) return rc;
+  if (!query || batch <= 0 || num_q_heads <= 0) return hipErrorInvalidValue;
+  if (batch > 65535 || num_q_heads > 65535) return hipErrorInvalidValue;
+  if (num_q_heads % cache->num_kv_heads) return hipErrorInvalidValue;
+  if (cache->page_table && cache->pt_batch_stride < 0) return hipErrorInvalidValue;
+  const int chunks = chunks_per_seq(cache);
+  int splits = num_splits > 0 ? num_splits : auto_splits(batch, num_q_heads, chunks);
+  splits = std::max(1, std::min(splits, std::max(chunks, 1)));
+  a->q = query;
+  a->q_b = q_batch_stride;
+  a->q_h = q_head_stride;
+  a->k_pages = cache->k_pages;
+  a->k_page = cache->k_page_stride;
+  a->k_head = cache->k_head_stride;
+  a->k_row = cache->k_row_stride;
+  a->v_pages = cache->v_pages;
+  a->v_page = cache->v_page_stride;
+  a->v_head = cache->v_head_stride;
+  a->v_row = cache->v_row_stride;
+  a->k_scale = cache->k_scale;
+  a->k_zp = cache->k_zp;
+  a->s_b = cache->s_batch_stride;
+  a->s_h = cache->s_head_stride;
+  a->s_g = cache->s_group_stride;
+  a->s_p = cache->s_page_stride;
+  a->page_table = cache->page_table;
+  a->pt_b = cache->pt_batch_stride;
+  a->seq_lens = cache->seq_lens;
+  a->page_lens = cache->page_lens;
+  a->pl_b = cache->pl_batch_stride;
+  a->page_rows = cache->page_rows;
+  a->pages_per_group = cache->pages_per_group;
+  a->max_pages = cache->max_pages;
+  a->hq_per_kv = num_q_heads / cache->num_kv_heads;
+  a->num_pages = cache->num_pages;
+  a->chunks_per_split = std::max(1, ceil_div(chunks, splits));
+  a->num_splits = splits;
+  a->num_q_heads = num_q_heads;
+  a->out = nullptr;
+  a->o_b = a->o_h = 0;
+  a->ws_acc = nullptr;
+  a->ws_ml = nullptr;
+  a->final_out = 0;
+  return hipSuccess;
+}
+
+int carve_partials(void* workspace, size_t workspace_bytes, int batch, int hq, int d,
+                   DecodeArgs* a) {
+  const size_t need = decode_ws_bytes(batch, hq, d, a->num_splits);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, kAlign))
+    return hipErrorInvalidValue;
+  const size_t n = (size_t)batch * hq * a->num_splits;
+  a->ws_acc = reinterpret_cast<float*>(workspace);
+  a->ws_ml = reinterpret_cast<double*>(reinterpret_cast<char*>(workspace) +
+                                       align_up(n * d * sizeof(float)));
+  return hipSuccess;
+}
+
+}  // namespace
+
+int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_batch_stride,
+                      int64_t q_head_stride, const fdi4_paged_cache* cache, float* out,
+                      int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  DecodeArgs a;
+  int rc = make_decode_args(query, batch, num_q_heads, q_batch_stride, q_head_stride, cache,
+                            num_splits, &a);
+  if (rc != hipSuccess) return rc;
+  if (!out) return hipErrorInvalidValue;
+  const int d = cache->head_dim;
+  a.out = out;
+  a.o_b = out_batch_stride;
+  a.o_h = out_head_stride;
+  if (a.num_splits == 1) {
+    a.final_out = 1;
+    return fdi4::launch_decode(a, d, cache->v_dtype, batch, stream);
+  }
+  rc = carve_partials(workspace, workspace_bytes, batch, num_q_heads, d, &a);
+  if (rc != hipSuccess) return rc;
+  hipError_t e = fdi4::launch_decode(a, d, cache->v_dtype, batch, stream);
+  if (e != hipSuccess) return e;
+  return fdi4::launch_merge(a.ws_acc, a.ws_ml, batch, num_q_heads, d, a.num_splits, out,
+                            out_batch_stride, out_head_stride, stream);
+}
+
+int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
+                               int64_t q_batch_stride, int64_t q_head_stride,
+                               const fdi4_paged_cache* cache, int num_splits, void* partials,
+                               size_t partials_bytes, hipStream_t stream) {
+  DecodeArgs a;
+  int rc = make_decode_args(query, batch, num_q_heads, q_batch_stride, q_head_stride, cache,
+                            num_splits, &a);
+  if (rc != hipSuccess) return rc;
+  if (a.num_splits != num_splits) return hipErrorInvalidValue;  // the layout must be exact
+  rc = carve_partials(partials, partials_bytes, batch, num_q_heads, cache->head_dim, &a);
+  if (rc != hipSuccess) return rc;
+  return fdi4::launch_decode(a, cache->head_dim, cache->v_dtype, batch, stream);
+}
+
+// ---- the reference's dense, shared-stream attention call ----------------------
+
+namespace {
+
+struct DenseLayout {
+  int dp;
+  size_t off_k, off_q, off_v, off_s, off_z, off_o, off_part, total;
+  int splits;
+};
+
+DenseLayout dense_layout(int B, int H, int D, int nb, int bs) {
+  DenseLayout L;
+  L.dp = padded_head_dim(D);
+  const bool pad = L.dp != D;
+  size_t off = 0;
+  L.off_k = off;
+  off += align_up((size_t)nb * bs * (L.dp / 2));
+  L.off_q = L.off_v = L.off_s = L.off_z = L.off_o = 0;
+  if (pad) {
+    L.off_q = off;
+    off += align_up((size_t)B * H * L.dp * sizeof(float));
+    L.off_v = off;
+    off += align_up((size_t)nb * bs * L.dp * sizeof(float));
+    L.off_s = off;
+    off += align_up((size_t)nb * L.dp * sizeof(float));
+    L.off_z = off;
+    off += align_up((size_t)nb * L.dp * sizeof(float));
+    L.off_o = off;
+    off += align_up((size_t)B * H * L.dp * sizeof(float));
+  }
+  L.splits = auto_splits(B, H, nb * ceil_div(bs, 16));
+  L.off_part = off;
+  off += decode_ws_bytes(B, H, L.dp, L.splits);
+  L.total = std::max<size_t>(off, kAlign);
+  return L;
+}
+
+bool dense_args_ok(int B, int H, int D, int nb, int bs) {
+  return B > 0 && H > 0 && D >= 1 && D <= 256 && nb >= 0 && bs >= 0 && B <= 65535 &&
+         H <= 65535;
+}
+
+}  // namespace
+
+size_t fdi4_flash_decode_int4_workspace_bytes(int batch_size, int num_heads, int head_dim,
+                                              int num_blocks, int block_size) {
+  if (!dense_args_ok(batch_size, num_heads, head_dim, num_blocks, block_size)) return 0;
+  return dense_layout(batch_size, num_heads, head_dim, num_blocks, block_size).total;
+}
+
+int fdi4_flash_decode_int4_ws(const float* query, const uint8_t* k_q, const float* k_scale,
+                              const float* k_zp, const float* value, const int* block_lens,
+                              int B, int H, int D, int nb, int bs, float* output,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!dense_args_ok(B, H, D, nb, bs) || !query || !output) return hipErrorInvalidValue;
+  if (nb == 0 || bs == 0) {
+    // No rows: the all-pages-empty case, exact zeros (a fill kernel, so the
+    // call stays capturable into a graph).
+    return fdi4::launch_pad_rows(output, (int64_t)B * H, 0, D, output, D, D, stream);
+  }
+  if (!k_q || !k_scale || !k_zp || !value || !block_lens) return hipErrorInvalidValue;
+  const DenseLayout L = dense_layout(B, H, D, nb, bs);
+  if (!workspace || workspace_bytes < L.total || !aligned(workspace, kAlign))
+    return hipErrorInvalidValue;
+  char* ws = reinterpret_cast<char*>(workspace);
+  const int dp = L.dp;
+  uint8_t* kp = reinterpret_cast<uint8_t*>(ws + L.off_k);
+  hipError_t e = fdi4::launch_pack(k_q, (int64_t)nb * bs, D, D, kp, dp / 2, dp / 2, stream);
+  if (e != hipSuccess) return e;
+  const float* q = query;
+  const float* v = value;
+  const float* s = k_scale;
+  const float* z = k_zp;
+  float* o = output;
+  if (dp != D) {
+    float* qp = reinterpret_cast<float*>(ws + L.off_q);
+    float* vp = reinterpret_cast<float*>(ws + L.off_v);
+    float* sp = reinterpret_cast<float*>(ws + L.off_s);
+    float* zp = reinterpret_cast<float*>(ws + L.off_z);
+    if ((e = fdi4::launch_pad_rows(query, (int64_t)B * H, D, D, qp, dp, dp, stream))) return e;
+    if ((e = fdi4::launch_pad_rows(value, (int64_t)nb * bs, D, D, vp, dp, dp, stream))) return e;
+    if ((e = fdi4::launch_pad_rows(k_scale, nb, D, D, sp, dp, dp, stream))) return e;
+    if ((e = fdi4::launch_pad_rows(k_zp, nb, D, D, zp, dp, dp, stream))) return e;
+    q = qp;
+    v = vp;
+    s = sp;
+    z = zp;
+    o = reinterpret_cast<float*>(ws + L.off_o);
+  }
+  fdi4_paged_cache c = {};
+  c.k_pages = kp;
+  c.k_page_stride = (int64_t)bs * (dp / 2);
+  c.k_head_stride = 0;
+  c.k_row_stride = dp / 2;
+  c.v_pages = const_cast<float*>(v);
+  c.v_dtype = FDI4_V_F32;
+  c.v_page_stride = (int64_t)bs * dp;
+  c.v_head_stride = 0;
+  c.v_row_stride = dp;
+  c.k_scale = const_cast<float*>(s);
+  c.k_zp = const_cast<float*>(z);
+  c.s_page_stride = dp;
+  c.page_table = nullptr;
+  c.seq_lens = nullptr;
+  c.page_lens = block_lens;
+  c.pl_batch_stride = 0;
+  c.num_kv_heads = 1;
+  c.head_dim = dp;
+  c.page_rows = bs;
+  c.pages_per_group = 1;
+  c.max_pages = nb;
+  c.num_pages = nb;
+  int rc = fdi4_decode_paged(q, B, H, (int64_t)H * dp, dp, &c, o, (int64_t)H * dp, dp, L.splits,
+                             ws + L.off_part, L.total - L.off_part, stream);
+  if (rc != hipSuccess) return rc;
+  if (dp != D) {
+    // Keep the first D channels: rows of dp floats back to rows of D floats.
+    return fdi4::launch_pad_rows(o, (int64_t)B * H, D, dp, output, D, D, stream);
+  }
+  return hipSuccess;
+}
+
+int fdi4_flash_decode_int4(const float* query, const uint8_t* k_q, const float* k_scale,
+                           const float* k_zp, const float* value, const int* block_lens,
+                           int batch_size, int num_heads, int head_dim, int num_blocks,
+                           int block_size, float* output, hipStream_t stream) {
+  if (!dense_args_ok(batch_size, num_heads, head_dim, num_blocks, block_size))
+    return hipErrorInvalidValue;
+  const size_t wsb = fdi4_flash_decode_int4_workspace_bytes(batch_size, num_heads, head_dim,
+                                                            num_blocks, block_size);
+  set_pool_threshold(stream);
+  void* ws = nullptr;
+  hipError_t e = hipMallocAsync(&ws, wsb, stream);
+  if (e != hipSuccess) return e;
+  int rc = fdi4_flash_decode_int4_ws(query, k_q, k_scale, k_zp, value, block_lens, batch_size,
+                                     num_heads, head_dim, num_blocks, block_size, output, ws, wsb,
+                                     stream);
+  hipError_t f = hipFreeAsync(ws, stream);
+  return rc != hipSuccess ? rc : f;
+}
+
+int fdi4_pack_int4(const uint8_t* q, int64_t rows, int num_channels, int64_t q_row_stride,
+                   uint8_t* out, int64_t out_row_stride, int out_cols, hipStream_t stream) {
+  if (!q || !out || rows < 0 || num_channels <= 0) return hipErrorInvalidValue;
+  if (out_cols < (num_channels + 1) / 2 || out_row_stride < out_cols ||
+      q_row_stride < num_channels)
+    return hipErrorInvalidValue;
+  return fdi4::launch_pack(q, rows, num_channels, q_row_stride, out, out_row_stride, out_cols,
+                           stream);
+}
+
+}  // extern "C"

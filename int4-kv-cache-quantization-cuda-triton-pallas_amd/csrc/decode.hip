@@ -1,0 +1,430 @@
+// Fused INT4 flash-decoding over paged, nibble-packed keys (gfx950).
+//
+// Semantics follow the reference page loop (src/flash_decode_ref.py:30-139,
+// the CUDA kernel csrc/flash_decode_int4.cu:104-221): unscaled logits q.k
+// with k = nib*scale - zp*scale, online softmax over the valid rows of every
+// page in logical order, empty pages skipped, out = acc / max(l, 1e-10).
+//
+// Work decomposition (split-K flash decoding):
+//   grid (num_splits, Hq, B); a workgroup of WAVES wave64s owns one split,
+//   a contiguous range of 16-row chunks of one (sequence, q-head); every wave
+//   takes a contiguous sub-range, keeps its own (m, l, acc) and the waves are
+//   merged through LDS. With one split the workgroup writes the output,
+//   otherwise (m, l, acc[D]) goes to the workspace and merge_kernel combines
+//   the splits with a log-sum-exp weighting.
+//
+// Per 16-row chunk and wave:
+//   K: LPT lanes per row, each lane one 8/16-byte load of packed nibbles
+//      (CPL channels). The logit is an fp64 dot product
+//          sum_d (q_d*s_d) * nib_d  -  sum_d q_d*(zp_d*s_d)
+//      whose products are exact in fp64; fp64 keeps the logit error ~1e-16
+//      relative, far below the float32 oracle's own ~1e-6 noise at D=128.
+//      (q_d*s_d) and the group constant are recomputed when the scale group
+//      changes; the scale/zero-point block of the next group is prefetched
+//      with one 16-byte load per lane and staged through LDS.
+//   softmax: wave-wide fp64 max over the chunk (DPP / ds_swizzle / permlane
+//      swaps), float32 exp of the fp64 differences.
+//   V: fully coalesced 16-byte loads (VPR lanes per row); the probabilities
+//      go through a 16-entry LDS row per wave; float32 FMA accumulation.
+//   The K and V loads of the next chunk are issued before the current chunk
+//   is computed (one chunk of software prefetch per wave). Rows past the
+//   valid count are loaded from the last valid row (never out of bounds) and
+//   masked to probability 0.
+
+#include "fdi4_device.hpp"
+#include "fdi4_internal.hpp"
+
+namespace fdi4 {
+
+template <int D, int VDT>
+struct Geo {
+  static constexpr int LPT = (D == 256) ? 8 : 4;   // lanes per key row
+  static constexpr int CPL = D / LPT;              // channels per lane (K)
+  static constexpr int KBL = CPL / 2;              // packed bytes per lane per row
+  static constexpr int KW = KBL / 4;               // 32-bit words per lane per row
+  static constexpr int TPW = 64 / LPT;             // key rows per sweep
+  static constexpr int KLD = 16 / TPW;             // key sweeps per chunk
+  static constexpr int VEB = VDT == kVF32 ? 4 : 2; // bytes per value element
+  static constexpr int VCL = 16 / VEB;             // value channels per lane
+  static constexpr int VPR = D / VCL;              // lanes per value row
+  static constexpr int RPL = 64 / VPR;             // value rows per sweep
+  static constexpr int VLD = 16 / RPL;             // value sweeps per chunk
+  static constexpr int SZI = D / 2;                // 16-byte items in a scale+zp block
+  static constexpr int SZL = (SZI + 63) / 64;      // scale+zp loads per lane
+  static_assert(RPL >= 1 && 16 % RPL == 0 && 16 % TPW == 0, "geometry");
+};
+
+template <int KW>
+struct KVec {
+  unsigned w[KW];
+};
+
+template <int KW>
+__device__ __forceinline__ KVec<KW> load_k(const uint8_t* p) {
+  KVec<KW> r;
+  if constexpr (KW == 4) {
+    const U32x4 v = ld16(p);
+    r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+  } else {
+    static_assert(KW == 2, "KW");
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = v.x; r.w[1] = v.y;
+  }
+  return r;
+}
+
+struct ChunkMeta {
+  int64_t phys;
+  int r0;
+  int nval;
+  int group;
+};
+
+__device__ __forceinline__ ChunkMeta chunk_meta(const DecodeArgs& a, int b, int T, int cpp,
+                                                int c) {
+  ChunkMeta m;
+  const int lp = c / cpp;
+  const int j = c - lp * cpp;
+  int rows;
+  if (a.page_lens) {
+    rows = min(max(a.page_lens[(int64_t)b * a.pl_b + lp], 0), a.page_rows);
+  } else {
+    rows = min(a.page_rows, T - lp * a.page_rows);
+  }
+  m.r0 = j * 16;
+  m.nval = min(16, rows - m.r0);
+  const int pg = a.page_table ? a.page_table[(int64_t)b * a.pt_b + lp] : lp;
+  m.phys = (int64_t)min(max(pg, 0), a.num_pages - 1);
+  m.group = lp / a.pages_per_group;
+  return m;
+}
+
+template <int D, int VDT, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
+  using G = Geo<D, VDT>;
+  constexpr int NT = WAVES * 64;
+
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / a.hq_per_kv;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // The wave index is uniform across the wave; saying so keeps the chunk loop
+  // counters in scalar registers and the page-table reads on the scalar unit.
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kq = lane % G::LPT;       // channel slice of this lane (K)
+  const int ktok = lane / G::LPT;     // key row within a sweep
+  const int vrow = lane / G::VPR;     // value row within a sweep
+  const int vcol = lane % G::VPR;     // value channel slice
+
+  __shared__ float q_s[D];
+  __shared__ float p_s[WAVES][16];
+  __shared__ float sz_s[WAVES][2 * D];
+  __shared__ float acc_s[WAVES][D];
+  __shared__ double m_s[WAVES];
+  __shared__ float l_s[WAVES];
+
+  for (int d = tid; d < D; d += NT) q_s[d] = a.q[(int64_t)b * a.q_b + (int64_t)h * a.q_h + d];
+  __syncthreads();
+
+  const int cpp = (a.page_rows + 15) >> 4;
+  int T, n_lp;
+  if (a.seq_lens) {
+    T = max(a.seq_lens[b], 0);
+    n_lp = min((T + a.page_rows - 1) / a.page_rows, a.max_pages);
+  } else {
+    n_lp = a.max_pages;
+    T = n_lp * a.page_rows;
+  }
+  const int n_chunks = n_lp * cpp;
+  const int c_begin = split * a.chunks_per_split;
+  const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
+  const int span = max(c_end - c_begin, 0);
+  const int per_wave = (span + WAVES - 1) / WAVES;
+  const int wc0 = c_begin + w * per_wave;
+  const int wc1 = min(wc0 + per_wave, c_end);
+
+  double m_run = -INFINITY;
+  float l_lane = 0.f;
+  float acc[G::VCL];
+#pragma unroll
+  for (int k = 0; k < G::VCL; ++k) acc[k] = 0.f;
+  double qs[G::CPL];
+  double cg = 0.0;
+  int cur_group = -1;
+
+  const float* sbase = a.k_scale + (int64_t)b * a.s_b + (int64_t)hk * a.s_h;
+  const float* zbase = a.k_zp + (int64_t)b * a.s_b + (int64_t)hk * a.s_h;
+  const uint8_t* kbase0 = a.k_pages + (int64_t)hk * a.k_head + kq * G::KBL;
+  const uint8_t* vbase0 = reinterpret_cast<const uint8_t*>(a.v_pages) +
+                          (int64_t)hk * a.v_head * G::VEB + vcol * 16;
+  const int64_t vrow_b = a.v_row * G::VEB;
+
+  // Scale/zero-point block of one group: items 0..D/4-1 are scale[4e..4e+3],
+  // items D/4..D/2-1 are zp. Lanes past the block reload an in-range item.
+  auto load_sz = [&](const ChunkMeta& m, U32x4* sz) {
+    const int64_t off = (int64_t)m.group * a.s_g + m.phys * a.s_p;
+#pragma unroll
+    for (int i = 0; i < G::SZL; ++i) {
+      const int e = (i * 64 + lane) % G::SZI;
+      const float* src = (e < D / 4) ? (sbase + off + 4 * e) : (zbase + off + 4 * (e - D / 4));
+      sz[i] = ld16(src);
+    }
+  };
+
+  auto load_chunk = [&](const ChunkMeta& m, KVec<G::KW>* kr, U32x4* vr) {
+    const uint8_t* kb = kbase0 + m.phys * a.k_page + (int64_t)m.r0 * a.k_row;
+#pragma unroll
+    for (int i = 0; i < G::KLD; ++i) {
+      const int t = max(min(i * G::TPW + ktok, m.nval - 1), 0);
+      kr[i] = load_k<G::KW>(kb + (int64_t)t * a.k_row);
+    }
+    const uint8_t* vb = vbase0 + (m.phys * a.v_page + (int64_t)m.r0 * a.v_row) * G::VEB;
+#pragma unroll
+    for (int i = 0; i < G::VLD; ++i) {
+      const int r = max(min(i * G::RPL + vrow, m.nval - 1), 0);
+      vr[i] = ld16(vb + (int64_t)r * vrow_b);
+    }
+  };
+
+  // One step: (1) stage a new scale group, (2) prefetch chunk c+1 into
+  // `nk/nv` (chunk c again on the last step, an L2-resident reload, so that
+  // every step issues the same loads and the wait counts stay exact),
+  // (3) read the page-table entry of chunk c+2 on the scalar unit,
+  // (4)-(6) consume chunk c from `ck/cv`. Called alternately with the two
+  // buffers swapped (a two-way unrolled ping-pong), so no register copy waits
+  // on the prefetch. An empty chunk (page_lens 0) is loaded from row 0 of its
+  // page and skipped.
+  int c = wc0;
+  ChunkMeta cm, nm;
+  U32x4 sz[G::SZL];
+  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, min(ci, wc1 - 1)); };
+  auto step = [&](const KVec<G::KW>* ck, const U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
+    if (cm.group != cur_group) {
+      float* szw = sz_s[w];
+#pragma unroll
+      for (int i = 0; i < G::SZL; ++i) {
+        const int e = i * 64 + lane;
+        if (e < G::SZI) *reinterpret_cast<U32x4*>(szw + 4 * e) = sz[i];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      double cgp = 0.0;
+#pragma unroll
+      for (int ci = 0; ci < G::CPL; ++ci) {
+        const int d = kq * G::CPL + ci;
+        const double qd = (double)q_s[d];
+        const double sd = (double)szw[d];
+        qs[ci] = qd * sd;
+        cgp = __builtin_fma(qd, (double)szw[D + d] * sd, cgp);
+      }
+      cg = allreduce_sum<1, G::LPT>(cgp);
+      cur_group = cm.group;
+      __builtin_amdgcn_wave_barrier();
+    }
+
+    const bool last = c + 1 >= wc1;
+    // Unconditional loads: a conditional load here makes the wait counts at
+    // the loop back-edge conservative (a full drain of the prefetch).
+    load_sz(nm, sz);
+    load_chunk(nm, nk, nv);
+    const ChunkMeta nnm = meta_at(c + 2);
+    if (cm.nval > 0) {
+
+    double lg[G::KLD];
+#pragma unroll
+    for (int i = 0; i < G::KLD; ++i) {
+      double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+#pragma unroll
+      for (int wi = 0; wi < G::KW; ++wi) {
+        const unsigned x = ck[i].w[wi];
+        s0 = __builtin_fma((double)(x & 15u), qs[wi * 8 + 0], s0);
+        s1 = __builtin_fma((double)((x >> 4) & 15u), qs[wi * 8 + 1], s1);
+        s2 = __builtin_fma((double)((x >> 8) & 15u), qs[wi * 8 + 2], s2);
+        s3 = __builtin_fma((double)((x >> 12) & 15u), qs[wi * 8 + 3], s3);
+        s0 = __builtin_fma((double)((x >> 16) & 15u), qs[wi * 8 + 4], s0);
+        s1 = __builtin_fma((double)((x >> 20) & 15u), qs[wi * 8 + 5], s1);
+        s2 = __builtin_fma((double)((x >> 24) & 15u), qs[wi * 8 + 6], s2);
+        s3 = __builtin_fma((double)(x >> 28), qs[wi * 8 + 7], s3);
+      }
+      double s = (s0 + s1) + (s2 + s3);
+      s = allreduce_sum<1, G::LPT>(s);
+      const int t = i * G::TPW + ktok;
+      lg[i] = (t < cm.nval) ? s - cg : -INFINITY;
+    }
+
+    double mc = lg[0];
+#pragma unroll
+    for (int i = 1; i < G::KLD; ++i) mc = fmax(mc, lg[i]);
+    mc = allreduce_max<G::LPT, 64>(mc);
+    const double m_new = fmax(m_run, mc);
+    const float corr = expf((float)(m_run - m_new));
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < G::KLD; ++i) {
+      const float p = expf((float)(lg[i] - m_new));
+      if (kq == 0) p_s[w][i * G::TPW + ktok] = p;
+      psum += p;
+    }
+    l_lane = l_lane * corr + (kq == 0 ? psum : 0.f);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+#pragma unroll
+    for (int k = 0; k < G::VCL; ++k) acc[k] *= corr;
+#pragma unroll
+    for (int i = 0; i < G::VLD; ++i) {
+      const int r = i * G::RPL + vrow;
+      const float p = (r < cm.nval) ? p_s[w][r] : 0.f;
+      if constexpr (VDT == kVF32) {
+        acc[0] = __builtin_fmaf(p, u2f(cv[i].x), acc[0]);
+        acc[1] = __builtin_fmaf(p, u2f(cv[i].y), acc[1]);
+        acc[2] = __builtin_fmaf(p, u2f(cv[i].z), acc[2]);
+        acc[3] = __builtin_fmaf(p, u2f(cv[i].w), acc[3]);
+      } else {
+        const unsigned u[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const _Float16 lo = __builtin_bit_cast(_Float16, (unsigned short)(u[k] & 0xFFFFu));
+          const _Float16 hi = __builtin_bit_cast(_Float16, (unsigned short)(u[k] >> 16));
+          acc[2 * k] = __builtin_fmaf(p, (float)lo, acc[2 * k]);
+          acc[2 * k + 1] = __builtin_fmaf(p, (float)hi, acc[2 * k + 1]);
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    }
+    c += 1;
+    cm = nm;
+    nm = nnm;
+    return last;
+  };
+
+  if (c < wc1) {
+    KVec<G::KW> ka[G::KLD], kb[G::KLD];
+    U32x4 va[G::VLD], vb[G::VLD];
+    cm = meta_at(c);
+    nm = meta_at(c + 1);
+    load_sz(cm, sz);
+    load_chunk(cm, ka, va);
+    while (true) {
+      if (step(ka, va, kb, vb)) break;
+      if (step(kb, vb, ka, va)) break;
+    }
+  }
+
+  // Wave totals: l over all lanes, acc over the lanes holding the same channels.
+  const float lw = allreduce_sum<1, 64>(l_lane);
+#pragma unroll
+  for (int k = 0; k < G::VCL; ++k) acc[k] = allreduce_sum<G::VPR, 64>(acc[k]);
+  if (lane < G::VPR) {
+#pragma unroll
+    for (int k = 0; k < G::VCL; ++k) acc_s[w][lane * G::VCL + k] = acc[k];
+  }
+  if (lane == 0) {
+    m_s[w] = m_run;
+    l_s[w] = lw;
+  }
+  __syncthreads();
+
+  double ms = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < WAVES; ++i) ms = fmax(ms, m_s[i]);
+  float ew[WAVES];
+  float l = 0.f;
+#pragma unroll
+  for (int i = 0; i < WAVES; ++i) {
+    ew[i] = (m_s[i] == -INFINITY) ? 0.f : expf((float)(m_s[i] - ms));
+    l = __builtin_fmaf(ew[i], l_s[i], l);
+  }
+  const int64_t pi = ((int64_t)b * a.num_q_heads + h) * a.num_splits + split;
+  for (int d = tid; d < D; d += NT) {
+    float o = 0.f;
+#pragma unroll
+    for (int i = 0; i < WAVES; ++i) o = __builtin_fmaf(ew[i], acc_s[i][d], o);
+    if (a.final_out) {
+      a.out[(int64_t)b * a.o_b + (int64_t)h * a.o_h + d] = o / fmaxf(l, 1e-10f);
+    } else {
+      a.ws_acc[pi * D + d] = o;
+    }
+  }
+  if (!a.final_out && tid == 0) {
+    a.ws_ml[2 * pi] = ms;
+    a.ws_ml[2 * pi + 1] = (double)l;
+  }
+}
+
+// Log-sum-exp merge of the split partials: grid (Hq, B), one thread per channel.
+template <int D>
+__global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ ws_acc,
+                                                  const double* __restrict__ ws_ml, int hq,
+                                                  int splits, float* __restrict__ out,
+                                                  int64_t o_b, int64_t o_h) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int64_t p0 = ((int64_t)b * hq + h) * splits;
+  double ms = -INFINITY;
+  for (int s = 0; s < splits; ++s) ms = fmax(ms, ws_ml[2 * (p0 + s)]);
+  float o = 0.f, l = 0.f;
+  for (int s = 0; s < splits; ++s) {
+    const double m = ws_ml[2 * (p0 + s)];
+    if (m == -INFINITY) continue;
+    const float e = expf((float)(m - ms));
+    o = __builtin_fmaf(e, ws_acc[(p0 + s) * D + d], o);
+    l = __builtin_fmaf(e, (float)ws_ml[2 * (p0 + s) + 1], l);
+  }
+  out[(int64_t)b * o_b + (int64_t)h * o_h + d] = o / fmaxf(l, 1e-10f);
+}
+
+constexpr int kDecodeWaves = 4;
+
+hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hipStream_t st) {
+  dim3 grid(a.num_splits, a.num_q_heads, batch);
+  dim3 block(kDecodeWaves * 64);
+#define FDI4_DEC(DD, VV)                                                                    \
+  if (D == DD && v_dtype == VV) {                                                           \
+    hipLaunchKernelGGL((decode_kernel<DD, VV, kDecodeWaves>), grid, block, 0, st, a);       \
+    return hipGetLastError();                                                               \
+  }
+  FDI4_DEC(64, kVF32) FDI4_DEC(128, kVF32) FDI4_DEC(256, kVF32)
+  FDI4_DEC(64, kVF16) FDI4_DEC(128, kVF16) FDI4_DEC(256, kVF16)
+#undef FDI4_DEC
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_merge(const float* ws_acc, const double* ws_ml, int batch, int hq, int D,
+                        int splits, float* out, int64_t o_b, int64_t o_h, hipStream_t st) {
+  dim3 grid(hq, batch);
+#define FDI4_MRG(DD)                                                                         \
+  if (D == DD) {                                                                             \
+    hipLaunchKernelGGL((merge_kernel<DD>), grid, dim3(DD), 0, st, ws_acc, ws_ml, hq, splits, \
+                       out, o_b, o_h);                                                       \
+    return hipGetLastError();                                                                \
+  }
+  FDI4_MRG(64) FDI4_MRG(128) FDI4_MRG(256)
+#undef FDI4_MRG
+  return hipErrorInvalidValue;
+}
+
+// Copy rows of `cols` floats into rows of `d_cols` floats, zero-filling the tail.
+__global__ __launch_bounds__(256) void pad_rows_kernel(const float* __restrict__ src, int64_t rows,
+                                                       int cols, int64_t s_stride,
+                                                       float* __restrict__ dst, int64_t d_stride,
+                                                       int d_cols) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * d_cols) return;
+  const int64_t r = idx / d_cols;
+  const int c = (int)(idx % d_cols);
+  dst[r * d_stride + c] = (c < cols) ? src[r * s_stride + c] : 0.f;
+}
+
+hipError_t launch_pad_rows(const float* src, int64_t rows, int cols, int64_t s_stride, float* dst,
+                           int64_t d_stride, int d_cols, hipStream_t st) {
+  const int64_t total = rows * d_cols;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                     src, rows, cols, s_stride, dst, d_stride, d_cols);
+  return hipGetLastError();
+}
+
+}  // namespace fdi4

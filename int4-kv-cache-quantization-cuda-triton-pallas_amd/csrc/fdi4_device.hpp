@@ -1,0 +1,132 @@
+// Device-side helpers shared by the INT4 quantizer and decode kernels (gfx950).
+//
+// Wave64 cross-lane primitives: DPP quad permutes for lane-xor 1/2, the
+// gfx950 permlane16/permlane32 swaps for the row and half-wave exchanges, and
+// ds_swizzle for the in-row xor 4/8 steps. 64-bit values move as two 32-bit
+// halves. Nothing here writes memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fdi4 {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ unsigned f2u(float x) { return __float_as_uint(x); }
+__device__ __forceinline__ float u2f(unsigned x) { return __uint_as_float(x); }
+
+union DU {
+  double d;
+  unsigned u[2];
+};
+
+// ---- lane-xor exchanges (value of lane ^ MASK) --------------------------------
+
+template <int MASK>
+__device__ __forceinline__ unsigned xchg_u32(unsigned x) {
+  if constexpr (MASK == 1) {
+    return (unsigned)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (MASK == 2) {
+    return (unsigned)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (MASK == 4 || MASK == 8) {
+    // ds_swizzle bit mode within 32 lanes: and 0x1F, or 0, xor MASK.
+    return (unsigned)__builtin_amdgcn_ds_swizzle((int)x, 0x1F | (MASK << 10));
+  } else if constexpr (MASK == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    // After the swap, r[0] holds the partner row for odd rows and r[1] for
+    // even rows; pick by the row parity of this lane.
+    return ((threadIdx.x & 16) ? r[0] : r[1]);
+  } else {
+    static_assert(MASK == 32, "unsupported lane mask");
+    auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return ((threadIdx.x & 32) ? r[0] : r[1]);
+  }
+}
+
+template <int MASK>
+__device__ __forceinline__ float xchg(float x) {
+  return u2f(xchg_u32<MASK>(f2u(x)));
+}
+
+template <int MASK>
+__device__ __forceinline__ double xchg(double x) {
+  DU v;
+  v.d = x;
+  v.u[0] = xchg_u32<MASK>(v.u[0]);
+  v.u[1] = xchg_u32<MASK>(v.u[1]);
+  return v.d;
+}
+
+// ---- butterfly all-reduce over the lanes selected by a mask range ------------
+
+template <int LO, int HI, typename T>
+__device__ __forceinline__ T allreduce_sum(T x) {
+  if constexpr (LO <= 1 && 1 < HI) x += xchg<1>(x);
+  if constexpr (LO <= 2 && 2 < HI) x += xchg<2>(x);
+  if constexpr (LO <= 4 && 4 < HI) x += xchg<4>(x);
+  if constexpr (LO <= 8 && 8 < HI) x += xchg<8>(x);
+  if constexpr (LO <= 16 && 16 < HI) x += xchg<16>(x);
+  if constexpr (LO <= 32 && 32 < HI) x += xchg<32>(x);
+  return x;
+}
+
+template <int LO, int HI, typename T>
+__device__ __forceinline__ T allreduce_max(T x) {
+  if constexpr (LO <= 1 && 1 < HI) x = fmax(x, xchg<1>(x));
+  if constexpr (LO <= 2 && 2 < HI) x = fmax(x, xchg<2>(x));
+  if constexpr (LO <= 4 && 4 < HI) x = fmax(x, xchg<4>(x));
+  if constexpr (LO <= 8 && 8 < HI) x = fmax(x, xchg<8>(x));
+  if constexpr (LO <= 16 && 16 < HI) x = fmax(x, xchg<16>(x));
+  if constexpr (LO <= 32 && 32 < HI) x = fmax(x, xchg<32>(x));
+  return x;
+}
+
+template <int LO, int HI>
+__device__ __forceinline__ float allreduce_min_f(float x) {
+  if constexpr (LO <= 1 && 1 < HI) x = fminf(x, xchg<1>(x));
+  if constexpr (LO <= 2 && 2 < HI) x = fminf(x, xchg<2>(x));
+  if constexpr (LO <= 4 && 4 < HI) x = fminf(x, xchg<4>(x));
+  if constexpr (LO <= 8 && 8 < HI) x = fminf(x, xchg<8>(x));
+  if constexpr (LO <= 16 && 16 < HI) x = fminf(x, xchg<16>(x));
+  if constexpr (LO <= 32 && 32 < HI) x = fminf(x, xchg<32>(x));
+  return x;
+}
+
+template <int LO, int HI>
+__device__ __forceinline__ float allreduce_max_f(float x) {
+  if constexpr (LO <= 1 && 1 < HI) x = fmaxf(x, xchg<1>(x));
+  if constexpr (LO <= 2 && 2 < HI) x = fmaxf(x, xchg<2>(x));
+  if constexpr (LO <= 4 && 4 < HI) x = fmaxf(x, xchg<4>(x));
+  if constexpr (LO <= 8 && 8 < HI) x = fmaxf(x, xchg<8>(x));
+  if constexpr (LO <= 16 && 16 < HI) x = fmaxf(x, xchg<16>(x));
+  if constexpr (LO <= 32 && 32 < HI) x = fmaxf(x, xchg<32>(x));
+  return x;
+}
+
+// ---- 16-byte global access ----------------------------------------------------
+
+struct alignas(16) U32x4 {
+  unsigned x, y, z, w;
+};
+
+__device__ __forceinline__ U32x4 ld16(const void* p) {
+  return *reinterpret_cast<const U32x4*>(p);
+}
+
+__device__ __forceinline__ void st16(void* p, U32x4 v) {
+  *reinterpret_cast<U32x4*>(p) = v;
+}
+
+// Non-temporal 16-byte load for data that is streamed exactly once.
+__device__ __forceinline__ U32x4 ld16_stream(const void* p) {
+  const U32x4* q = reinterpret_cast<const U32x4*>(p);
+  U32x4 r;
+  r.x = __builtin_nontemporal_load(&q->x);
+  r.y = __builtin_nontemporal_load(&q->y);
+  r.z = __builtin_nontemporal_load(&q->z);
+  r.w = __builtin_nontemporal_load(&q->w);
+  return r;
+}
+
+}  // namespace fdi4

@@ -1,0 +1,75 @@
+// Kernel argument blocks and launcher declarations shared by the HIP
+// translation units and the C-ABI layer. Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fdi4 {
+
+enum VDtype : int { kVF32 = 0, kVF16 = 1 };
+
+// Grouped paged quantizer: keys [B, H, T, D] (any strides, channel stride 1)
+// into packed pages and group scales.
+struct QuantPagedArgs {
+  const float* k;
+  int64_t k_b, k_h, k_t;                // elements
+  const int32_t* seq_lens;              // [B]
+  const int32_t* page_table;            // [B, pt_b]
+  int64_t pt_b;
+  uint8_t* k_pages;
+  int64_t kp_page, kp_head, kp_row;     // bytes
+  float* scale;
+  float* zp;
+  int64_t s_b, s_h, s_g;                // elements
+  int page_rows;
+  int num_pages;                        // physical pages; table entries are clamped
+  int max_tokens;                       // rows of k; sequence lengths are clamped to it
+};
+
+// Split-K paged decode.
+struct DecodeArgs {
+  const float* q;
+  int64_t q_b, q_h;                     // elements
+  const uint8_t* k_pages;
+  int64_t k_page, k_head, k_row;        // bytes
+  const void* v_pages;
+  int64_t v_page, v_head, v_row;        // elements
+  const float* k_scale;
+  const float* k_zp;
+  int64_t s_b, s_h, s_g, s_p;           // elements
+  const int32_t* page_table;            // null: logical page == physical page
+  int64_t pt_b;
+  const int32_t* seq_lens;              // null: every sequence spans max_pages pages
+  const int32_t* page_lens;             // null: rows from seq_lens
+  int64_t pl_b;
+  int page_rows, pages_per_group, max_pages, hq_per_kv, num_pages;
+  int chunks_per_split, num_splits, num_q_heads;
+  int final_out;                        // 1: normalized output; 0: split partials
+  float* out;
+  int64_t o_b, o_h;
+  float* ws_acc;                        // [B, Hq, S, D]
+  double* ws_ml;                        // [B, Hq, S, 2] = (m, l)
+};
+
+hipError_t launch_quantize_rows(const float* kv, int64_t rows, int C, int64_t stride, uint8_t* q,
+                                int64_t q_stride, bool packed, float* scale_out, float* zp_out,
+                                void* ws, hipStream_t st);
+size_t rows_workspace_bytes(int64_t rows, int C);
+
+hipError_t launch_quantize_paged(const QuantPagedArgs& a, int D, int group, int batch, int heads,
+                                 int max_tokens, hipStream_t st);
+
+hipError_t launch_pack(const uint8_t* q, int64_t rows, int C, int64_t q_stride, uint8_t* out,
+                       int64_t o_stride, int out_cols, hipStream_t st);
+
+hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hipStream_t st);
+
+hipError_t launch_merge(const float* ws_acc, const double* ws_ml, int batch, int hq, int D,
+                        int splits, float* out, int64_t o_b, int64_t o_h, hipStream_t st);
+
+hipError_t launch_pad_rows(const float* src, int64_t rows, int cols, int64_t s_stride, float* dst,
+                           int64_t d_stride, int d_cols, hipStream_t st);
+
+}  // namespace fdi4

@@ -1,0 +1,314 @@
+// INT4 key quantizer kernels for gfx950.
+//
+// Arithmetic (bit-exact with the NumPy quantizer, reference
+// src/quantize_int4_ref.py:46-84): per channel over the group's valid rows,
+//   mn, mx = min, max                     (exact)
+//   span   = fmaxf(mx - mn, 1e-8f)        (float32 floor, as NumPy casts 1e-8)
+//   scale  = span / 15.0f                 (IEEE division)
+//   zp     = (-mn) / scale                (IEEE division)
+//   q      = clamp(rintf((x - mn) / scale), 0, 15)   (round half to even)
+// This file is compiled with -ffp-contract=off and without fast-math so that
+// every operation above is one correctly rounded float32 operation.
+//
+// Kernels
+//   rows_minmax_kernel / rows_finalize_kernel / rows_quantize_kernel
+//       the 2-D contract: one scale group over all rows of [rows, C]
+//       (reference csrc/flash_decode_int4.cu:27-83), split over row tiles so
+//       that any row count fills the chip; unpacked or nibble-packed output.
+//   quantize_paged_kernel<D, GROUP>
+//       one workgroup per (group, kv-head, sequence): 16-byte token-major
+//       loads held in registers, wave64 min/max reduction, quantize from
+//       registers, nibble pack, and 16-byte stores of whole page rows through
+//       the page table.
+//   pack_kernel   device form of the nibble packing (reference src/int4_pack.py:14-29)
+
+#include "fdi4_device.hpp"
+#include "fdi4_internal.hpp"
+
+namespace fdi4 {
+
+__device__ __forceinline__ unsigned quant_bin(float x, float mn, float scale) {
+  float b = rintf((x - mn) / scale);
+  b = fminf(fmaxf(b, 0.0f), 15.0f);
+  return (unsigned)b;
+}
+
+__device__ __forceinline__ void scale_zp(float mn, float mx, float* s, float* z) {
+  const float span = fmaxf(mx - mn, 1e-8f);
+  *s = span / 15.0f;
+  *z = (-mn) / *s;
+}
+
+// ---------------------------------------------------------------------------
+// 2-D contract: [rows, C] row-major, one group over all rows.
+// ---------------------------------------------------------------------------
+
+constexpr int kRowsThreads = 256;
+constexpr int kRowsTile = 256;  // rows per partial
+
+// grid (ceil(C/64), n_tiles); lane -> channel, wave -> row phase.
+__global__ __launch_bounds__(kRowsThreads) void rows_minmax_kernel(
+    const float* __restrict__ kv, int64_t rows, int C, int64_t stride,
+    float2* __restrict__ partial) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  const int64_t r0 = (int64_t)blockIdx.y * kRowsTile;
+  const int64_t r1 = min(r0 + kRowsTile, rows);
+  float mn = INFINITY, mx = -INFINITY;
+  if (c < C) {
+    for (int64_t r = r0 + wv; r < r1; r += kRowsThreads / 64) {
+      const float x = kv[r * stride + c];
+      mn = fminf(mn, x);
+      mx = fmaxf(mx, x);
+    }
+  }
+  __shared__ float smn[kRowsThreads / 64][64], smx[kRowsThreads / 64][64];
+  smn[wv][lane] = mn;
+  smx[wv][lane] = mx;
+  __syncthreads();
+  if (wv == 0 && c < C) {
+#pragma unroll
+    for (int w = 1; w < kRowsThreads / 64; ++w) {
+      mn = fminf(mn, smn[w][lane]);
+      mx = fmaxf(mx, smx[w][lane]);
+    }
+    partial[(int64_t)blockIdx.y * C + c] = make_float2(mn, mx);
+  }
+}
+
+// grid ceil(C/256): thread -> channel.
+__global__ __launch_bounds__(256) void rows_finalize_kernel(
+    const float2* __restrict__ partial, int n_tiles, int C, float* __restrict__ scale_out,
+    float* __restrict__ zp_out, float2* __restrict__ mn_scale) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  float mn = INFINITY, mx = -INFINITY;
+  for (int t = 0; t < n_tiles; ++t) {
+    const float2 p = partial[(int64_t)t * C + c];
+    mn = fminf(mn, p.x);
+    mx = fmaxf(mx, p.y);
+  }
+  float s, z;
+  scale_zp(mn, mx, &s, &z);
+  scale_out[c] = s;
+  zp_out[c] = z;
+  mn_scale[c] = make_float2(mn, s);
+}
+
+// Unpacked: grid (ceil(C/64), ceil(rows/kRowsTile)); lane -> channel.
+// Packed:   grid (ceil(ceil(C/2)/64), ...);           lane -> output byte.
+template <bool PACKED>
+__global__ __launch_bounds__(kRowsThreads) void rows_quantize_kernel(
+    const float* __restrict__ kv, int64_t rows, int C, int64_t stride,
+    const float2* __restrict__ mn_scale, uint8_t* __restrict__ q, int64_t q_stride) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int j = blockIdx.x * 64 + lane;
+  const int64_t r0 = (int64_t)blockIdx.y * kRowsTile;
+  const int64_t r1 = min(r0 + kRowsTile, rows);
+  if (!PACKED) {
+    if (j >= C) return;
+    const float2 ms = mn_scale[j];
+    for (int64_t r = r0 + wv; r < r1; r += kRowsThreads / 64)
+      q[r * q_stride + j] = (uint8_t)quant_bin(kv[r * stride + j], ms.x, ms.y);
+  } else {
+    const int c0 = 2 * j, c1 = 2 * j + 1;
+    if (c0 >= C) return;
+    const float2 m0 = mn_scale[c0];
+    const bool has1 = c1 < C;
+    const float2 m1 = has1 ? mn_scale[c1] : make_float2(0.f, 1.f);
+    for (int64_t r = r0 + wv; r < r1; r += kRowsThreads / 64) {
+      const unsigned lo = quant_bin(kv[r * stride + c0], m0.x, m0.y);
+      const unsigned hi = has1 ? quant_bin(kv[r * stride + c1], m1.x, m1.y) : 0u;
+      q[r * q_stride + j] = (uint8_t)(lo | (hi << 4));
+    }
+  }
+}
+
+size_t rows_workspace_bytes(int64_t rows, int C) {
+  const int64_t tiles = (rows + kRowsTile - 1) / kRowsTile;
+  return (size_t)(tiles * C + C) * sizeof(float2);
+}
+
+hipError_t launch_quantize_rows(const float* kv, int64_t rows, int C, int64_t stride,
+                                uint8_t* q, int64_t q_stride, bool packed, float* scale_out,
+                                float* zp_out, void* ws, hipStream_t st) {
+  const int64_t tiles = (rows + kRowsTile - 1) / kRowsTile;
+  float2* partial = reinterpret_cast<float2*>(ws);
+  float2* mn_scale = partial + tiles * C;
+  dim3 g1((C + 63) / 64, (unsigned)tiles);
+  hipLaunchKernelGGL(rows_minmax_kernel, g1, dim3(kRowsThreads), 0, st, kv, rows, C, stride,
+                     partial);
+  hipLaunchKernelGGL(rows_finalize_kernel, dim3((C + 255) / 256), dim3(256), 0, st, partial,
+                     (int)tiles, C, scale_out, zp_out, mn_scale);
+  if (packed) {
+    const int nbytes = (C + 1) / 2;
+    dim3 g3((nbytes + 63) / 64, (unsigned)tiles);
+    hipLaunchKernelGGL(rows_quantize_kernel<true>, g3, dim3(kRowsThreads), 0, st, kv, rows, C,
+                       stride, mn_scale, q, q_stride);
+  } else {
+    dim3 g3((C + 63) / 64, (unsigned)tiles);
+    hipLaunchKernelGGL(rows_quantize_kernel<false>, g3, dim3(kRowsThreads), 0, st, kv, rows, C,
+                       stride, mn_scale, q, q_stride);
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Grouped, paged, packed quantizer.
+// ---------------------------------------------------------------------------
+
+constexpr int kQThreads = 256;
+
+// One workgroup quantizes the rows [g*GROUP, min((g+1)*GROUP, T_b)) of one
+// (sequence b, kv-head h). Thread t owns channels 4*(t % VPR) .. +3 of the
+// rows t / VPR + i * RPI, i < NI; one 16-byte load per owned row.
+template <int D, int GROUP>
+__global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArgs a) {
+  constexpr int VPR = D / 4;              // threads per row (16 B each)
+  constexpr int RPI = kQThreads / VPR;    // rows covered per sweep
+  constexpr int NI = GROUP / RPI;         // rows per thread
+  constexpr int RB = D / 2;               // packed bytes per row
+  constexpr int NWAVE = kQThreads / 64;
+  static_assert(VPR <= 64 && GROUP % RPI == 0, "layout");
+
+  const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int T = min(a.seq_lens[b], a.max_tokens);
+  const int r0 = g * GROUP;
+  if (r0 >= T) return;
+  const int nrows = min(GROUP, T - r0);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int cq = tid % VPR, rsub = tid / VPR;
+
+  const float* src = a.k + (int64_t)b * a.k_b + (int64_t)h * a.k_h + (int64_t)r0 * a.k_t + 4 * cq;
+  float4 x[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int r = rsub + i * RPI;
+    if (r < nrows) x[i] = *reinterpret_cast<const float4*>(src + (int64_t)r * a.k_t);
+  }
+
+  float mn[4], mx[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    mn[k] = INFINITY;
+    mx[k] = -INFINITY;
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    if (rsub + i * RPI < nrows) {
+      mn[0] = fminf(mn[0], x[i].x); mx[0] = fmaxf(mx[0], x[i].x);
+      mn[1] = fminf(mn[1], x[i].y); mx[1] = fmaxf(mx[1], x[i].y);
+      mn[2] = fminf(mn[2], x[i].z); mx[2] = fmaxf(mx[2], x[i].z);
+      mn[3] = fminf(mn[3], x[i].w); mx[3] = fmaxf(mx[3], x[i].w);
+    }
+  }
+  // Lanes of one wave that own the same channels differ in the bits >= VPR.
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    mn[k] = allreduce_min_f<VPR, 64>(mn[k]);
+    mx[k] = allreduce_max_f<VPR, 64>(mx[k]);
+  }
+  __shared__ float4 s_mn[NWAVE][VPR], s_mx[NWAVE][VPR];
+  if (lane < VPR) {
+    s_mn[wv][lane] = make_float4(mn[0], mn[1], mn[2], mn[3]);
+    s_mx[wv][lane] = make_float4(mx[0], mx[1], mx[2], mx[3]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    const float4 pm = s_mn[w][cq], px = s_mx[w][cq];
+    mn[0] = fminf(mn[0], pm.x); mx[0] = fmaxf(mx[0], px.x);
+    mn[1] = fminf(mn[1], pm.y); mx[1] = fmaxf(mx[1], px.y);
+    mn[2] = fminf(mn[2], pm.z); mx[2] = fmaxf(mx[2], px.z);
+    mn[3] = fminf(mn[3], pm.w); mx[3] = fmaxf(mx[3], px.w);
+  }
+  float sc[4], zp[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) scale_zp(mn[k], mx[k], &sc[k], &zp[k]);
+  if (rsub == 0) {
+    const int64_t so = (int64_t)b * a.s_b + (int64_t)h * a.s_h + (int64_t)g * a.s_g + 4 * cq;
+    *reinterpret_cast<float4*>(a.scale + so) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+    *reinterpret_cast<float4*>(a.zp + so) = make_float4(zp[0], zp[1], zp[2], zp[3]);
+  }
+
+  // Quantize from registers; two bytes (channels 4cq..4cq+3) per owned row.
+  __shared__ uint16_t s_out[GROUP * RB / 2];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int r = rsub + i * RPI;
+    if (r < nrows) {
+      const unsigned n0 = quant_bin(x[i].x, mn[0], sc[0]);
+      const unsigned n1 = quant_bin(x[i].y, mn[1], sc[1]);
+      const unsigned n2 = quant_bin(x[i].z, mn[2], sc[2]);
+      const unsigned n3 = quant_bin(x[i].w, mn[3], sc[3]);
+      s_out[r * (RB / 2) + cq] = (uint16_t)(n0 | (n1 << 4) | (n2 << 8) | (n3 << 12));
+    }
+  }
+  __syncthreads();
+
+  // Whole 16-byte pieces of packed rows to their pages.
+  constexpr int PPR = RB / 16;            // 16-byte pieces per packed row
+  constexpr int NPIECE = GROUP * PPR;
+  for (int pc = tid; pc < NPIECE; pc += kQThreads) {
+    const int r = pc / PPR, part = pc % PPR;
+    if (r >= nrows) continue;
+    const int tok = r0 + r;
+    const int lp = tok / a.page_rows, row = tok % a.page_rows;
+    const int64_t phys =
+        (int64_t)min(max(a.page_table[(int64_t)b * a.pt_b + lp], 0), a.num_pages - 1);
+    uint8_t* dst = a.k_pages + phys * a.kp_page + (int64_t)h * a.kp_head + (int64_t)row * a.kp_row +
+                   part * 16;
+    st16(dst, *reinterpret_cast<const U32x4*>(reinterpret_cast<const uint8_t*>(s_out) +
+                                              r * RB + part * 16));
+  }
+}
+
+hipError_t launch_quantize_paged(const QuantPagedArgs& a, int D, int group, int batch, int heads,
+                                 int max_tokens, hipStream_t st) {
+  const int ngroups = (max_tokens + group - 1) / group;
+  if (ngroups == 0 || batch == 0 || heads == 0) return hipSuccess;
+  dim3 grid(ngroups, heads, batch);
+#define FDI4_QP(DD, GG)                                                                  \
+  if (D == DD && group == GG) {                                                          \
+    hipLaunchKernelGGL((quantize_paged_kernel<DD, GG>), grid, dim3(kQThreads), 0, st, a); \
+    return hipGetLastError();                                                            \
+  }
+  FDI4_QP(64, 64) FDI4_QP(64, 128) FDI4_QP(64, 256)
+  FDI4_QP(128, 64) FDI4_QP(128, 128) FDI4_QP(128, 256)
+  FDI4_QP(256, 64) FDI4_QP(256, 128) FDI4_QP(256, 256)
+#undef FDI4_QP
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Device nibble packing: out[r, j] = q[r, 2j] | q[r, 2j+1] << 4 for
+// j < ceil(C/2); bytes ceil(C/2) .. out_cols-1 are zero (row padding).
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void pack_kernel(const uint8_t* __restrict__ q, int64_t rows,
+                                                   int C, int64_t q_stride,
+                                                   uint8_t* __restrict__ out, int64_t o_stride,
+                                                   int out_cols) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = rows * out_cols;
+  if (idx >= total) return;
+  const int64_t r = idx / out_cols;
+  const int j = (int)(idx % out_cols);
+  const int c0 = 2 * j, c1 = 2 * j + 1;
+  unsigned v = 0;
+  if (c0 < C) v = q[r * q_stride + c0] & 0xF;
+  if (c1 < C) v |= (q[r * q_stride + c1] & 0xF) << 4;
+  out[r * o_stride + j] = (uint8_t)v;
+}
+
+hipError_t launch_pack(const uint8_t* q, int64_t rows, int C, int64_t q_stride, uint8_t* out,
+                       int64_t o_stride, int out_cols, hipStream_t st) {
+  const int64_t total = rows * out_cols;
+  if (total == 0) return hipSuccess;
+  const int64_t blocks = (total + 255) / 256;
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)blocks), dim3(256), 0, st, q, rows, C, q_stride,
+                     out, o_stride, out_cols);
+  return hipGetLastError();
+}
+
+}  // namespace fdi4

@@ -1,0 +1,98 @@
+"""ctypes view of libfdi4's C ABI (include/fdi4.h).
+
+For callers that hold raw device pointers and no torch binding (the shape a
+cgo / JNI / N-API binding of the reference's cu_* functions would take).
+Loading the library needs no GPU; calling a compute entry point does.
+"""
+
+import ctypes
+import os
+
+from ._lib import LIB_PATH
+
+c_int, c_int32, c_int64, c_size_t, c_void_p = (ctypes.c_int, ctypes.c_int32, ctypes.c_int64,
+                                                ctypes.c_size_t, ctypes.c_void_p)
+
+V_F32 = 0
+V_F16 = 1
+
+
+class PagedCache(ctypes.Structure):
+    """Mirror of ``fdi4_paged_cache``."""
+    _fields_ = [
+        ("k_pages", c_void_p),
+        ("k_page_stride", c_int64), ("k_head_stride", c_int64), ("k_row_stride", c_int64),
+        ("v_pages", c_void_p),
+        ("v_dtype", c_int32),
+        ("v_page_stride", c_int64), ("v_head_stride", c_int64), ("v_row_stride", c_int64),
+        ("k_scale", c_void_p),
+        ("k_zp", c_void_p),
+        ("s_batch_stride", c_int64), ("s_head_stride", c_int64),
+        ("s_group_stride", c_int64), ("s_page_stride", c_int64),
+        ("page_table", c_void_p),
+        ("pt_batch_stride", c_int64),
+        ("seq_lens", c_void_p),
+        ("page_lens", c_void_p),
+        ("pl_batch_stride", c_int64),
+        ("num_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("page_rows", c_int32),
+        ("pages_per_group", c_int32),
+        ("max_pages", c_int32),
+        ("num_pages", c_int32),
+    ]
+
+
+#: name -> (restype, argtypes); the complete exported surface of include/fdi4.h.
+SIGNATURES = {
+    "fdi4_abi_version": (c_int, []),
+    "fdi4_error_string": (ctypes.c_char_p, [c_int]),
+    "fdi4_quantize_int4": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p,
+                                   c_void_p]),
+    "fdi4_quantize_rows_workspace_bytes": (c_size_t, [c_int64, c_int]),
+    "fdi4_quantize_rows": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_int64, c_int,
+                                   c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "fdi4_quantize_paged": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64, c_int64, c_int,
+                                    ctypes.POINTER(PagedCache), c_void_p]),
+    "fdi4_flash_decode_int4": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
+                                       c_void_p]),
+    "fdi4_flash_decode_int4_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "fdi4_flash_decode_int4_ws": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                          c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
+                                          c_void_p, c_size_t, c_void_p]),
+    "fdi4_decode_num_splits": (c_int, [c_int, c_int, ctypes.POINTER(PagedCache)]),
+    "fdi4_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "fdi4_decode_paged": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64,
+                                  ctypes.POINTER(PagedCache), c_void_p, c_int64, c_int64, c_int,
+                                  c_void_p, c_size_t, c_void_p]),
+    "fdi4_merge_splits": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
+                                  c_int64, c_int64, c_void_p]),
+    "fdi4_pack_int4": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_int64, c_int,
+                               c_void_p]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """dlopen libfdi4.so and attach the prototypes (no GPU needed)."""
+    global _lib
+    if _lib is not None and path == LIB_PATH:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run `python -m flash_decode_int4._build`")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path == LIB_PATH:
+        _lib = lib
+    return lib
+
+
+def check(rc: int, what: str = "fdi4 call") -> None:
+    if rc != 0:
+        msg = load().fdi4_error_string(rc)
+        raise RuntimeError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")

@@ -1,0 +1,151 @@
+"""GPU parity of the HIP quantizers against the oracle: bit-exact bins, packed
+bytes, scales and zero-points (the north star's bar; the reference itself
+held its CUDA/Triton quantizers only to "<= 1 bin on < 1%")."""
+
+import numpy as np
+import pytest
+
+from oracle import pack_int4, quantize_groups_ref, quantize_int4_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from flash_decode_int4 import ops
+    return ops
+
+
+class TestRowsQuantizer:
+    """The 2-D contract: one group over all rows (reference src/ops.py:111-161)."""
+
+    @pytest.mark.parametrize("shape", [(1, 1), (1, 64), (255, 3), (256, 3), (257, 3),
+                                       (1030, 8), (4096, 128), (512, 128), (32768, 128),
+                                       (3, 1000)])
+    def test_bit_exact(self, shape):
+        kv = np.random.RandomState(shape[0]).randn(*shape).astype(np.float32)
+        q, scale, zp = _ops().quantize_int4(kv, backend="hip")
+        qr, sr, zr = quantize_int4_ref(kv)
+        np.testing.assert_array_equal(q, qr)
+        assert scale.tobytes() == sr.tobytes()
+        np.testing.assert_array_equal(zp, zr)
+
+    def test_ties_round_half_to_even(self):
+        col = np.array([0.0, 15.0, 0.5, 1.5, 2.5, 3.5, 14.5, 7.5, 8.5], dtype=np.float32)
+        q, s, z = _ops().quantize_int4(np.tile(col[:, None], (1, 5)), backend="hip")
+        np.testing.assert_array_equal(q[:, 0], [0, 15, 0, 2, 2, 4, 14, 8, 8])
+
+    def test_uniform_channel_floor(self):
+        kv = np.full((64, 16), 5.0, dtype=np.float32)
+        q, s, z = _ops().quantize_int4(kv, backend="cuda")
+        qr, sr, zr = quantize_int4_ref(kv)
+        np.testing.assert_array_equal(q, qr)
+        np.testing.assert_array_equal(s, sr)
+
+    def test_higher_rank_auto_backend(self):
+        kv = np.random.RandomState(4).randn(4, 8, 64).astype(np.float32)
+        q, s, z = _ops().quantize_int4(kv)
+        qr, sr, zr = quantize_int4_ref(kv)
+        np.testing.assert_array_equal(q, qr)
+        np.testing.assert_array_equal(s, sr)
+
+    def test_named_backend_rejects_3d(self):
+        with pytest.raises(ValueError, match="2D"):
+            _ops().quantize_int4(np.zeros((2, 3, 4), np.float32), backend="hip")
+
+    def test_binding_rejects_bad_quantizer_input(self):
+        """reference tests/test_ops_dispatch.py:321-328."""
+        import torch
+        C = _ops()._C
+        with pytest.raises(RuntimeError, match="float32"):
+            C.quantize_int4(torch.zeros(4, 4, dtype=torch.float64, device="cuda"))
+        with pytest.raises(RuntimeError, match="non-empty"):
+            C.quantize_int4(torch.zeros(0, 4, device="cuda"))
+        with pytest.raises(RuntimeError, match="2D"):
+            C.quantize_int4(torch.zeros(4, device="cuda"))
+
+    def test_packed_rows_into_strided_view(self):
+        import torch
+        kv = np.random.RandomState(8).randn(40, 33).astype(np.float32)
+        pool = torch.zeros(3, 64, 24, dtype=torch.uint8, device="cuda")
+        s = torch.zeros(33, device="cuda")
+        z = torch.zeros(33, device="cuda")
+        _ops()._C.quantize_rows_into(torch.from_numpy(kv).cuda(), pool[1, :40], s, z, True)
+        qr, sr, zr = quantize_int4_ref(kv)
+        got = pool.cpu().numpy()
+        np.testing.assert_array_equal(got[1, :40, :17], pack_int4(qr))
+        assert not got[0].any() and not got[2].any() and not got[1, 40:].any()
+        assert not got[1, :, 17:].any()
+        np.testing.assert_array_equal(s.cpu().numpy(), sr)
+
+
+class TestDevicePack:
+
+    @pytest.mark.parametrize("shape", [(10, 7), (256, 64), (3, 1), (1000, 128)])
+    def test_matches_host_pack(self, shape):
+        import torch
+        q = np.random.RandomState(shape[1]).randint(0, 16, shape).astype(np.uint8)
+        got = _ops().pack_int4_device(torch.from_numpy(q).cuda()).cpu().numpy()
+        np.testing.assert_array_equal(got, pack_int4(q))
+
+
+def _paged_keys(B, H, D, lens, seed, group=128):
+    import torch
+    from flash_decode_int4.workloads import page_layout
+    rng = np.random.RandomState(seed)
+    T = max(max(lens), 1)
+    k = rng.randn(B, H, T, D).astype(np.float32)
+    table, P = page_layout(lens, 16, seed)
+    dev = torch.device("cuda")
+    G = (T + group - 1) // group
+    kp = torch.zeros(P, H, 16, D // 2, dtype=torch.uint8, device=dev)
+    s = torch.zeros(B, H, G, D, device=dev)
+    z = torch.zeros(B, H, G, D, device=dev)
+    _ops().quantize_int4_paged(torch.from_numpy(k).to(dev),
+                               torch.tensor(lens, dtype=torch.int32, device=dev),
+                               torch.from_numpy(table).to(dev), kp, s, z, group)
+    return k, table, kp.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy()
+
+
+class TestPagedQuantizer:
+
+    @pytest.mark.parametrize("B,H,D,lens,group", [
+        (1, 4, 64, [512], 128),
+        (3, 2, 128, [0, 37, 300], 128),
+        (2, 3, 128, [2048, 1999], 128),
+        (2, 2, 256, [129, 256], 128),
+        (2, 2, 128, [100, 513], 64),
+        (1, 2, 64, [700], 256),
+    ])
+    def test_bit_exact_pages_and_scales(self, B, H, D, lens, group):
+        k, table, kp, s, z = _paged_keys(B, H, D, lens, seed=B * 100 + D, group=group)
+        qr, sr, zr = quantize_groups_ref(k, np.array(lens), group_size=group)
+        for b in range(B):
+            ng = (lens[b] + group - 1) // group
+            np.testing.assert_array_equal(s[b, :, :ng], sr[b, :, :ng])
+            np.testing.assert_array_equal(z[b, :, :ng], zr[b, :, :ng])
+            for lp in range((lens[b] + 15) // 16):
+                n = min(16, lens[b] - lp * 16)
+                want = pack_int4(qr[b, :, lp * 16:lp * 16 + n])
+                np.testing.assert_array_equal(kp[table[b, lp], :, :n], want)
+
+    def test_outlier_channels_bit_exact(self):
+        import torch
+        from flash_decode_int4.workloads import make_workload
+        w = make_workload(batch=2, heads=4, head_dim=128, tokens=300, rope=True, outliers=4,
+                          seed=9)
+        dev = torch.device("cuda")
+        G = 3
+        kp = torch.zeros(w["num_pages"], 4, 16, 64, dtype=torch.uint8, device=dev)
+        s = torch.zeros(2, 4, G, 128, device=dev)
+        z = torch.zeros(2, 4, G, 128, device=dev)
+        _ops().quantize_int4_paged(torch.from_numpy(w["k"]).to(dev),
+                                   torch.from_numpy(w["seq_lens"]).to(dev),
+                                   torch.from_numpy(w["page_table"]).to(dev), kp, s, z, 128)
+        qr, sr, zr = quantize_groups_ref(w["k"], w["seq_lens"])
+        np.testing.assert_array_equal(s.cpu().numpy(), sr)
+        kpn = kp.cpu().numpy()
+        for b in range(2):
+            for lp in range(19):
+                n = min(16, 300 - lp * 16)
+                np.testing.assert_array_equal(kpn[w["page_table"][b, lp], :, :n],
+                                              pack_int4(qr[b, :, lp * 16:lp * 16 + n]))
