@@ -1,0 +1,411 @@
+#!/usr/bin/env python3
+"""Benchmark of the INT4 paged decode path on one MI355X.
+
+Metric: fused INT4 decode attention time (us) and its fraction of the HBM
+roofline at B8 x H32 x D128 x 2048 tokens (16-token pages, 128-token scale
+groups, fp32 values), plus the grouped quantizer's GB/s.
+
+A step is one decode of the whole batch: the split-K decode kernel plus the
+split merge, on inputs already resident in HBM. Input sets are rotated so
+their total exceeds twice the 256 MB Infinity Cache (nothing is served from
+the cache across steps). The quantizer is timed in its own loop over the same
+rotation. HIP events on the launch stream time each kernel; wall clock times
+the K steps. Bytes are algorithmic (valid tokens only): packed K T*D/2, V
+T*D*4, scale and zero-point ceil(T/128)*D*8 per (sequence, head), the page
+table, sequence lengths, q and the output.
+
+The cpu_baseline leg times the NumPy oracle (the reference's page loop, one
+call per (sequence, head) stream, one BLAS thread) on this host's cores over
+the same workload and uses its output as the parity check of the GPU result.
+
+Prints ONE JSON line. Options: --workload (anchor, sweep_512 ... llama,
+ragged), --splits, --value-dtype float16, --no-cpu, --pmc (HBM traffic of the
+decode kernel from two rocprofv3 --pmc child runs).
+"""
+
+import argparse
+import json
+import math
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.join(ROOT, "int4-kv-cache-quantization-cuda-triton-pallas_amd")
+if PKG_ROOT not in sys.path:
+    sys.path.insert(0, PKG_ROOT)
+
+METRIC = ("fused INT4 decode attn µs + % HBM peak @B8×H32×D128×2048; "
+          "quantizer GB/s")
+HBM_PEAK_GBS = 8000.0
+INFINITY_CACHE = 256 * 2 ** 20
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", default="anchor")
+    p.add_argument("--splits", type=int, default=0, help="0 = the library's choice")
+    p.add_argument("--value-dtype", default="float32", choices=["float32", "float16"])
+    p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    p.add_argument("--cpu-runs", type=int, default=3)
+    p.add_argument("--pmc", action="store_true",
+                   help="measure HBM traffic per decode launch with rocprofv3 --pmc")
+    p.add_argument("--pmc-child", default="", help=argparse.SUPPRESS)
+    return p.parse_args()
+
+
+def build_sets(name, value_dtype, n_sets_hint=0):
+    """Independent input sets in HBM (different seeds), keys quantized into pages."""
+    import torch
+    from flash_decode_int4 import ops, workloads
+    sets = []
+    first = workloads.make_workload(name, value_dtype=value_dtype, backend="torch", seed=1234)
+    vbytes = 2 if value_dtype == "float16" else 4
+    set_bytes = workloads.decode_bytes(first["seq_lens"], first["heads"], first["head_dim"],
+                                       vbytes)
+    if n_sets_hint:
+        n_sets = n_sets_hint
+    else:
+        n_sets = max(2, math.ceil(2 * INFINITY_CACHE / set_bytes) + 1)
+    for i in range(n_sets):
+        # Same lengths (and so the same bytes) in every set; different data.
+        w = first if i == 0 else workloads.make_workload(
+            name, seq_lens=first["seq_lens"], value_dtype=value_dtype, backend="torch",
+            seed=1234 + 101 * i)
+        dev = torch.device("cuda")
+        B, H, D = w["batch"], w["heads"], w["head_dim"]
+        G = (w["max_tokens"] + w["group_rows"] - 1) // w["group_rows"]
+        s = dict(
+            q=w["q"], k=w["k"], v=w["v_pages"],
+            kp=torch.zeros(w["num_pages"], H, w["page_rows"], D // 2, dtype=torch.uint8,
+                           device=dev),
+            s=torch.zeros(B, H, G, D, device=dev),
+            z=torch.zeros(B, H, G, D, device=dev),
+            pt=torch.as_tensor(w["page_table"], device=dev),
+            sl=torch.as_tensor(w["seq_lens"], device=dev),
+            w=w)
+        ops.quantize_int4_paged(s["k"], s["sl"], s["pt"], s["kp"], s["s"], s["z"],
+                                w["group_rows"])
+        sets.append(s)
+    torch.cuda.synchronize()
+    return sets, set_bytes
+
+
+def time_decode(sets, splits, steps, warmup):
+    import torch
+    from flash_decode_int4._lib import load_binding
+    C = load_binding()
+    w0 = sets[0]["w"]
+    B, H, D = w0["batch"], w0["heads"], w0["head_dim"]
+    ppg = w0["group_rows"] // w0["page_rows"]
+    maxp = w0["page_table"].shape[1]
+    S = splits or int(C.decode_num_splits(B, H, maxp, w0["page_rows"]))
+    S = max(1, min(S, maxp * ((w0["page_rows"] + 15) // 16)))
+    parts = torch.empty(int(C.decode_partials_bytes(B, H, D, S)), dtype=torch.uint8,
+                        device="cuda")
+
+    def step(i, ev=None):
+        # The production call: with one split it is the decode kernel alone
+        # (writing the output); with several it is the decode kernel and the
+        # merge, issued here as the same two launches so each can be timed.
+        st = sets[i % len(sets)]
+        if ev is not None:
+            ev[0].record()
+        if S == 1:
+            out = C.decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
+                                 st["sl"], None, ppg, maxp, 1)
+            if ev is not None:
+                ev[1].record()
+                ev[2].record()
+            return out
+        C.decode_paged_partials(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
+                                st["sl"], None, ppg, maxp, S, parts)
+        if ev is not None:
+            ev[1].record()
+        out = C.merge_splits(parts, B, H, D, S)
+        if ev is not None:
+            ev[2].record()
+        return out
+
+    for i in range(warmup):
+        step(i)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        out = step(i, evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dec = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
+    mrg = [e[1].elapsed_time(e[2]) * 1e3 for e in evs]
+    tot = [e[0].elapsed_time(e[2]) * 1e3 for e in evs]
+    return dict(splits=S, wall_s=wall, decode_us=dec, merge_us=mrg, step_us=tot,
+                last_out=out, last_set=(steps - 1) % len(sets))
+
+
+def time_quantizer(sets, steps, warmup):
+    import torch
+    from flash_decode_int4 import ops
+    g = sets[0]["w"]["group_rows"]
+
+    def q(i):
+        st = sets[i % len(sets)]
+        ops.quantize_int4_paged(st["k"], st["sl"], st["pt"], st["kp"], st["s"], st["z"], g)
+
+    for i in range(warmup):
+        q(i)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        evs[i][0].record()
+        q(i)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) * 1e3 for a, b in evs]
+
+
+def median(x):
+    s = sorted(x)
+    n = len(s)
+    return s[n // 2] if n % 2 else 0.5 * (s[n // 2 - 1] + s[n // 2])
+
+
+def cpu_baseline(st, gpu_out, runs, vbytes):
+    """Time the NumPy oracle on the host over the same workload; check the GPU output."""
+    import numpy as np
+    import torch
+    from oracle import cref, paged_decode_ref, quantize_groups_ref, pack_int4
+    from flash_decode_int4 import workloads
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    w = st["w"]
+    host = dict(q=st["q"].cpu().numpy(), kp=st["kp"].cpu().numpy(),
+                v=st["v"].float().cpu().numpy(), s=st["s"].cpu().numpy(),
+                z=st["z"].cpu().numpy(), pt=w["page_table"], sl=w["seq_lens"])
+    k_host = st["k"].cpu().numpy()
+    args = (host["q"], host["kp"], host["v"], host["s"], host["z"], host["pt"], host["sl"])
+    ctx = threadpool_limits(limits=1) if threadpool_limits else None
+    times, qtimes = [], []
+    try:
+        if ctx is not None:
+            ctx.__enter__()
+        for _ in range(max(1, runs)):
+            t0 = time.perf_counter()
+            o32 = paged_decode_ref(*args)
+            times.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        qr, sr, zr = quantize_groups_ref(k_host, host["sl"])
+        qtimes.append(time.perf_counter() - t0)
+    finally:
+        if ctx is not None:
+            ctx.__exit__(None, None, None)
+    o64 = cref.paged_attention_f64(*args)
+    got = gpu_out.cpu().numpy()
+    # Quantizer parity: scales and every packed page of this set, bit for bit.
+    scales_ok = bool(np.array_equal(host["s"], sr) and np.array_equal(host["z"], zr))
+    pages_ok = True
+    for b in range(len(host["sl"])):
+        n = int(host["sl"][b])
+        for lp in range((n + 15) // 16):
+            rows = min(16, n - lp * 16)
+            want = pack_int4(qr[b, :, lp * 16:lp * 16 + rows])
+            if not np.array_equal(host["kp"][host["pt"][b, lp], :, :rows], want):
+                pages_ok = False
+                break
+        if not pages_ok:
+            break
+    nbytes = workloads.decode_bytes(host["sl"], w["heads"], w["head_dim"], vbytes)
+    qbytes = workloads.quantize_bytes(host["sl"], w["heads"], w["head_dim"])
+    t = median(times)
+    base = {
+        "value": round(nbytes / t / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"whole workload: NumPy oracle page loop, one call per (sequence, head) "
+                   f"stream, {len(times)} runs, median {t * 1e3:.1f} ms per decode; "
+                   f"quantizer oracle {qtimes[0] * 1e3:.1f} ms "
+                   f"({qbytes / qtimes[0] / 1e9:.3f} GB/s); BLAS limited to 1 thread; "
+                   f"host cores available {len(os.sched_getaffinity(0))}"),
+        "decode_ms": round(t * 1e3, 3),
+        "quantizer_ms": round(qtimes[0] * 1e3, 3),
+    }
+    parity = {
+        "max_abs_vs_oracle_f32": float(np.abs(got - o32).max()),
+        "max_abs_vs_f64": float(np.abs(got - o64).max()),
+        "oracle_f32_vs_f64": float(np.abs(o32 - o64).max()),
+        "tolerance": 1e-5,
+        "quantizer_bit_exact": bool(scales_ok and pages_ok),
+    }
+    return base, parity
+
+
+def pmc_child(args):
+    """Run a few decode launches on one set (for rocprofv3 --pmc); also a
+    256 MiB device copy whose counters calibrate the bytes/counter factor."""
+    import torch
+    sets, _ = build_sets(args.workload, args.value_dtype, n_sets_hint=1)
+    r = time_decode(sets, args.splits, steps=3, warmup=1)
+    a = torch.empty(64 * 2 ** 20, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1.0)
+    for _ in range(3):
+        torch.mul(a, 1.0, out=b)  # an elementwise kernel: reads 256 MiB, writes 256 MiB
+    torch.cuda.synchronize()
+    print(json.dumps({"splits": r["splits"]}))
+
+
+def pmc_traffic(args):
+    """HBM bytes per decode-kernel launch from FETCH_SIZE and WRITE_SIZE passes,
+    each scaled by the same counter's reading for a 256 MiB copy kernel."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not found"
+    import csv
+    out = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="fdi4_pmc_")
+        cmd = [exe, "--pmc", counter, "-d", d, "-o", "pmc", "--output-format", "csv", "--",
+               sys.executable, os.path.abspath(__file__), "--workload", args.workload,
+               "--splits", str(args.splits), "--value-dtype", args.value_dtype,
+               "--pmc-child", counter]
+        try:
+            subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=180,
+                           check=False)
+        except subprocess.TimeoutExpired:
+            return None, f"rocprofv3 --pmc {counter} timed out"
+        rows = []
+        for dirpath, _, files in os.walk(d):
+            for f in files:
+                if f.endswith("counter_collection.csv"):
+                    with open(os.path.join(dirpath, f)) as fh:
+                        rows += list(csv.DictReader(fh))
+        dec = [float(r["Counter_Value"]) for r in rows
+               if "decode_kernel" in r.get("Kernel_Name", "")
+               and r.get("Counter_Name") == counter]
+        cpy = [float(r["Counter_Value"]) for r in rows
+               if "MulFunctor" in r.get("Kernel_Name", "")
+               and r.get("Counter_Name") == counter]
+        shutil.rmtree(d, ignore_errors=True)
+        if not dec or not cpy:
+            return None, f"no {counter} rows for the decode or copy kernel"
+        out[counter] = (median(dec), max(cpy))
+    # A 256 MiB copy reads and writes 256 MiB: the factor converts counter units to bytes.
+    copy_bytes = 256 * 2 ** 20
+    fetch = out["FETCH_SIZE"][0] * copy_bytes / out["FETCH_SIZE"][1]
+    write = out["WRITE_SIZE"][0] * copy_bytes / out["WRITE_SIZE"][1]
+    return {"fetch_bytes": fetch, "write_bytes": write,
+            "fetch_factor_bytes_per_unit": copy_bytes / out["FETCH_SIZE"][1],
+            "write_factor_bytes_per_unit": copy_bytes / out["WRITE_SIZE"][1]}, None
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU (the decode path shards by sequence "
+              f"and head with no exchange); --gpus {args.gpus} / WORLD_SIZE {world} is not "
+              f"supported", file=sys.stderr)
+        sys.exit(2)
+    if args.pmc_child:
+        pmc_child(args)
+        return
+    import torch
+    from flash_decode_int4 import ops, workloads
+    if not ops.HAS_HIP:
+        print("bench.py: the HIP extension or the GPU is unavailable: "
+              f"{ops.backend_status()}", file=sys.stderr)
+        sys.exit(1)
+
+    sets, set_bytes = build_sets(args.workload, args.value_dtype)
+    w0 = sets[0]["w"]
+    vbytes = 2 if args.value_dtype == "float16" else 4
+    qbytes = workloads.quantize_bytes(w0["seq_lens"], w0["heads"], w0["head_dim"])
+
+    # Correctness before timing: the timed two-call path equals the one-call
+    # path, and a different split count gives the same answer.
+    st0 = sets[0]
+    ref1 = ops.flash_decode_paged(st0["q"], st0["kp"], st0["v"], st0["s"], st0["z"], st0["pt"],
+                                  st0["sl"], num_splits=1)
+    r = time_decode([st0], args.splits, steps=1, warmup=0)
+    gate = float((r["last_out"] - ref1).abs().max())
+    if not (math.isfinite(gate) and gate < 2e-6 and bool(torch.isfinite(ref1).all())):
+        print(f"bench.py: correctness gate failed (split vs single-split diff {gate})",
+              file=sys.stderr)
+        sys.exit(1)
+
+    res = time_decode(sets, args.splits, args.steps, args.warmup)
+    qt = time_quantizer(sets, args.steps, args.warmup)
+    dec_us = sum(res["decode_us"]) / len(res["decode_us"])
+    mrg_us = sum(res["merge_us"]) / len(res["merge_us"])
+    step_us = sum(res["step_us"]) / len(res["step_us"])
+    ms_per_step = res["wall_s"] / args.steps * 1e3
+    q_us = sum(qt) / len(qt)
+
+    line = {
+        "metric": METRIC,
+        "value": round(set_bytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (f64 logit accumulation)" if vbytes == 4 else "f32 with f16 values",
+        "data": "synthetic N(0,1) q/K/V, seeded; keys quantized on the GPU; random page "
+                "permutation",
+        "config": {
+            "workload": (f"{args.workload}: B{w0['batch']} H{w0['heads']} D{w0['head_dim']} "
+                         f"T{int(max(w0['seq_lens']))}, {w0['page_rows']}-token pages, "
+                         f"{w0['group_rows']}-token scale groups, {args.value_dtype} values"),
+            "batch": w0["batch"], "heads": w0["heads"], "head_dim": w0["head_dim"],
+            "max_tokens": int(max(w0["seq_lens"])), "page_rows": w0["page_rows"],
+            "group_rows": w0["group_rows"], "num_splits": res["splits"],
+            "input_sets": len(sets), "bytes_per_step": set_bytes,
+        },
+        "decode_us": round(step_us, 3),
+        "decode_kernel_us": round(dec_us, 3),
+        "merge_us": round(mrg_us, 3),
+        "decode_us_median": round(median(res["step_us"]), 3),
+        "hbm_frac": round(set_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "quantizer_us": round(q_us, 3),
+        "quantizer_gbs": round(qbytes / (q_us * 1e-6) / 1e9, 2),
+        "quantizer_hbm_frac": round(qbytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(set_bytes / (dec_us * 1e-6) / 1e9, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(set_bytes / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": f"decode_kernel<D={w0['head_dim']}, {args.value_dtype} values>",
+        },
+    }
+    if args.pmc:
+        traffic, err = pmc_traffic(args)
+        if traffic is not None:
+            line["roofline"]["traffic"] = round(traffic["fetch_bytes"] + traffic["write_bytes"])
+            line["roofline"]["traffic_detail"] = {k: round(v, 4) for k, v in traffic.items()}
+        else:
+            line["roofline"]["traffic_error"] = err
+    if not args.no_cpu:
+        st = sets[res["last_set"]]
+        base, parity = cpu_baseline(st, res["last_out"], args.cpu_runs, vbytes)
+        line["cpu_baseline"] = base
+        line["parity"] = parity
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

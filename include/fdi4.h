@@ -157,6 +157,22 @@ int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_
                       int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Bytes of the split partials for fdi4_decode_paged_partials: part_acc
+ * float [B, Hq, S, D] at offset 0, then part_ml double [B, Hq, S, 2] = (m, l)
+ * at offset round_up(B*Hq*S*D*4, 256). */
+size_t fdi4_decode_partials_bytes(int batch, int num_q_heads, int head_dim, int num_splits);
+
+/* The decode kernel alone: writes the per-split partials (the layout of
+ * fdi4_decode_partials_bytes) instead of the output; num_splits >= 1 and at
+ * most one split per 16-row chunk of the longest sequence. With
+ * fdi4_merge_splits this is fdi4_decode_paged in two calls -- for timing the
+ * kernels separately, and for split-K across devices (gather the partials,
+ * then merge once). */
+int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
+                               int64_t q_batch_stride, int64_t q_head_stride,
+                               const fdi4_paged_cache* cache, int num_splits, void* partials,
+                               size_t partials_bytes, hipStream_t stream);
+
 /* Log-sum-exp merge of split partials part_acc [B, Hq, S, D] fp32 and
  * part_ml [B, Hq, S, 2] fp64 (m, l), as written by fdi4_decode_paged, into
  * out. Exposed so that partials gathered from several devices can be merged.

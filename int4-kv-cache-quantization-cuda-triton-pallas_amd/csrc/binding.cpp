@@ -298,6 +298,70 @@ torch::Tensor decode_paged(torch::Tensor query, torch::Tensor k_pages, torch::Te
   return out;
 }
 
+// Decode kernel alone into a caller-provided partials buffer (uint8 tensor of
+// at least fdi4_decode_partials_bytes); see merge_splits.
+void decode_paged_partials(torch::Tensor query, torch::Tensor k_pages, torch::Tensor v_pages,
+                           torch::Tensor k_scale, torch::Tensor k_zp,
+                           c10::optional<torch::Tensor> page_table,
+                           c10::optional<torch::Tensor> seq_lens,
+                           c10::optional<torch::Tensor> page_lens, int64_t pages_per_group,
+                           int64_t max_pages, int64_t num_splits, torch::Tensor partials) {
+  CHECK_DEV(query);
+  CHECK_INPUT(partials);
+  TORCH_CHECK(query.scalar_type() == torch::kFloat32 && query.dim() == 3 && query.stride(2) == 1,
+              "query must be float32 [batch, heads, head_dim] with contiguous rows");
+  TORCH_CHECK(query.size(2) == k_pages.size(3) * 2, "query head_dim must match the cache");
+  TORCH_CHECK(num_splits >= 1, "num_splits must be >= 1");
+  fdi4_paged_cache c = make_cache(k_pages, &v_pages, k_scale, k_zp, page_table, seq_lens,
+                                  page_lens, pages_per_group, max_pages);
+  const int B = (int)query.size(0), Hq = (int)query.size(1), D = (int)query.size(2);
+  if (k_scale.dim() == 4) {
+    TORCH_CHECK(k_scale.size(0) >= B && k_scale.size(2) * pages_per_group >= max_pages,
+                "k_scale too small for the batch / pages");
+  }
+  if (page_table && page_table->defined())
+    TORCH_CHECK(page_table->size(0) >= B, "page_table must have a row per sequence");
+  if (seq_lens && seq_lens->defined())
+    TORCH_CHECK(seq_lens->size(0) >= B, "seq_lens must have an entry per sequence");
+  if (page_lens && page_lens->defined())
+    TORCH_CHECK(page_lens->size(0) >= B, "page_lens must have a row per sequence");
+  TORCH_CHECK(Hq % k_pages.size(1) == 0, "query heads must be a multiple of kv_heads");
+  const size_t need = fdi4_decode_partials_bytes(B, Hq, D, (int)num_splits);
+  TORCH_CHECK(partials.scalar_type() == torch::kUInt8 && (size_t)partials.numel() >= need,
+              "partials must be a uint8 buffer of at least ", need, " bytes");
+  check_rc(fdi4_decode_paged_partials(query.data_ptr<float>(), B, Hq, query.stride(0),
+                                      query.stride(1), &c, (int)num_splits, partials.data_ptr(),
+                                      partials.numel(), stream()),
+           "decode_paged_partials");
+}
+
+torch::Tensor merge_splits(torch::Tensor partials, int64_t batch, int64_t q_heads,
+                           int64_t head_dim, int64_t num_splits) {
+  CHECK_INPUT(partials);
+  const size_t need =
+      fdi4_decode_partials_bytes((int)batch, (int)q_heads, (int)head_dim, (int)num_splits);
+  TORCH_CHECK(need > 0 && partials.scalar_type() == torch::kUInt8 &&
+                  (size_t)partials.numel() >= need,
+              "partials must be a uint8 buffer of at least ", need, " bytes");
+  auto out = torch::empty({batch, q_heads, head_dim},
+                          partials.options().dtype(torch::kFloat32));
+  const size_t acc_bytes = (size_t)batch * q_heads * num_splits * head_dim * sizeof(float);
+  const size_t ml_off = (acc_bytes + 255) / 256 * 256;
+  const auto* base = reinterpret_cast<const char*>(partials.data_ptr());
+  check_rc(fdi4_merge_splits(reinterpret_cast<const float*>(base),
+                             reinterpret_cast<const double*>(base + ml_off), (int)batch,
+                             (int)q_heads, (int)head_dim, (int)num_splits, out.data_ptr<float>(),
+                             out.stride(0), out.stride(1), stream()),
+           "merge_splits");
+  return out;
+}
+
+int64_t decode_partials_bytes(int64_t batch, int64_t q_heads, int64_t head_dim,
+                              int64_t num_splits) {
+  return (int64_t)fdi4_decode_partials_bytes((int)batch, (int)q_heads, (int)head_dim,
+                                             (int)num_splits);
+}
+
 int64_t decode_num_splits(int64_t batch, int64_t q_heads, int64_t max_pages, int64_t page_rows) {
   fdi4_paged_cache c = {};
   c.max_pages = (int32_t)max_pages;
@@ -329,6 +393,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("quantize_rows_into", &quantize_rows_into, "One-group INT4 quantization into views (HIP)");
   m.def("quantize_paged", &quantize_paged, "Grouped INT4 key quantization into packed pages (HIP)");
   m.def("decode_paged", &decode_paged, "Split-K INT4 flash decoding over paged keys (HIP)");
+  m.def("decode_paged_partials", &decode_paged_partials,
+        "Decode kernel alone, writing split partials (HIP)");
+  m.def("merge_splits", &merge_splits, "Log-sum-exp merge of split partials (HIP)");
+  m.def("decode_partials_bytes", &decode_partials_bytes, "Bytes of the split partials");
   m.def("decode_num_splits", &decode_num_splits, "Split count chosen for a decode shape");
   m.def("pack_int4", &pack_int4, "Device nibble packing (HIP)");
   m.def("abi_version", &fdi4_abi_version, "C ABI version of the loaded libfdi4");

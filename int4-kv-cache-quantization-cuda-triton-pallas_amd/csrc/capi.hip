@@ -7,6 +7,7 @@
 // carving.
 
 #include <limits.h>
+#include <stdlib.h>
 
 #include <algorithm>
 
@@ -18,9 +19,13 @@ namespace {
 using fdi4::DecodeArgs;
 using fdi4::QuantPagedArgs;
 
-constexpr int kWaves = 4;          // waves per decode workgroup
-constexpr int kTargetWgs = 2048;   // decode workgroups aimed for (8 per CU on 256 CUs)
-constexpr int kMinChunksPerWave = 2;
+// Decode launch shape. A workgroup has 4 or 8 wave64s; the split count is the
+// smallest that gives about kTargetWaves resident waves (8 per CU on 256 CUs,
+// the occupancy the decode kernel's ~200 VGPRs allow), so that with enough
+// (sequence, head) streams no split -- and no merge kernel -- is needed.
+// FDI4_DECODE_WAVES and FDI4_DECODE_TARGET_WAVES override the choice (tuning).
+constexpr int kTargetWaves = 2048;
+constexpr int kMinChunksPerWave = 4;
 constexpr size_t kAlign = 256;
 
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
@@ -35,11 +40,26 @@ int chunks_per_seq(const fdi4_paged_cache* c) {
   return c->max_pages * ceil_div(c->page_rows, 16);
 }
 
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  if (!v || !*v) return dflt;
+  const int x = atoi(v);
+  return x > 0 ? x : dflt;
+}
+
+int pick_waves(int chunks) {
+  const int w = env_int("FDI4_DECODE_WAVES", 0);
+  if (w == 4 || w == 8) return w;
+  return chunks >= 8 * 2 * kMinChunksPerWave ? 8 : 4;
+}
+
 int auto_splits(int batch, int hq, int chunks) {
   if (chunks <= 0) return 1;
-  const int64_t bh = (int64_t)batch * hq;
-  int s = (int)((kTargetWgs + bh - 1) / bh);
-  const int smax = std::max(1, chunks / (kWaves * kMinChunksPerWave));
+  const int waves = pick_waves(chunks);
+  const int64_t target = env_int("FDI4_DECODE_TARGET_WAVES", kTargetWaves);
+  const int64_t per_split = (int64_t)batch * hq * waves;
+  int s = (int)((target + per_split - 1) / per_split);
+  const int smax = std::max(1, chunks / (waves * kMinChunksPerWave));
   return std::max(1, std::min(s, smax));
 }
 
@@ -253,6 +273,7 @@ int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_b
   a->ws_acc = nullptr;
   a->ws_ml = nullptr;
   a->final_out = 0;
+  a->waves = pick_waves(chunks);
   return hipSuccess;
 }
 

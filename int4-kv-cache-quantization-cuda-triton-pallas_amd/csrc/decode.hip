@@ -122,9 +122,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   __shared__ double m_s[WAVES];
   __shared__ float l_s[WAVES];
 
-  for (int d = tid; d < D; d += NT) q_s[d] = a.q[(int64_t)b * a.q_b + (int64_t)h * a.q_h + d];
-  __syncthreads();
-
   const int cpp = (a.page_rows + 15) >> 4;
   int T, n_lp;
   if (a.seq_lens) {
@@ -301,13 +298,24 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     return last;
   };
 
-  if (c < wc1) {
-    KVec<G::KW> ka[G::KLD], kb[G::KLD];
-    U32x4 va[G::VLD], vb[G::VLD];
+  // q is loaded first (one element per thread, D <= NT), then the first
+  // chunk's loads are issued, then q is staged in LDS: the chunk latency
+  // overlaps the q load and the workgroup barrier, and waiting for q (the
+  // oldest load) does not wait for the chunk.
+  static_assert(D <= NT, "one query element per thread");
+  const float qv = (tid < D) ? a.q[(int64_t)b * a.q_b + (int64_t)h * a.q_h + tid] : 0.f;
+  const bool has_work = c < wc1;
+  KVec<G::KW> ka[G::KLD], kb[G::KLD];
+  U32x4 va[G::VLD], vb[G::VLD];
+  if (has_work) {
     cm = meta_at(c);
     nm = meta_at(c + 1);
     load_sz(cm, sz);
     load_chunk(cm, ka, va);
+  }
+  if (tid < D) q_s[tid] = qv;
+  __syncthreads();
+  if (has_work) {
     while (true) {
       if (step(ka, va, kb, vb)) break;
       if (step(kb, vb, ka, va)) break;
@@ -376,18 +384,17 @@ __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ ws_a
   out[(int64_t)b * o_b + (int64_t)h * o_h + d] = o / fmaxf(l, 1e-10f);
 }
 
-constexpr int kDecodeWaves = 4;
-
 hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hipStream_t st) {
   dim3 grid(a.num_splits, a.num_q_heads, batch);
-  dim3 block(kDecodeWaves * 64);
-#define FDI4_DEC(DD, VV)                                                                    \
-  if (D == DD && v_dtype == VV) {                                                           \
-    hipLaunchKernelGGL((decode_kernel<DD, VV, kDecodeWaves>), grid, block, 0, st, a);       \
-    return hipGetLastError();                                                               \
+#define FDI4_DEC(DD, VV, WW)                                                             \
+  if (D == DD && v_dtype == VV && a.waves == WW) {                                       \
+    hipLaunchKernelGGL((decode_kernel<DD, VV, WW>), grid, dim3(WW * 64), 0, st, a);      \
+    return hipGetLastError();                                                            \
   }
-  FDI4_DEC(64, kVF32) FDI4_DEC(128, kVF32) FDI4_DEC(256, kVF32)
-  FDI4_DEC(64, kVF16) FDI4_DEC(128, kVF16) FDI4_DEC(256, kVF16)
+  FDI4_DEC(64, kVF32, 4) FDI4_DEC(128, kVF32, 4) FDI4_DEC(256, kVF32, 4)
+  FDI4_DEC(64, kVF16, 4) FDI4_DEC(128, kVF16, 4) FDI4_DEC(256, kVF16, 4)
+  FDI4_DEC(64, kVF32, 8) FDI4_DEC(128, kVF32, 8) FDI4_DEC(256, kVF32, 8)
+  FDI4_DEC(64, kVF16, 8) FDI4_DEC(128, kVF16, 8) FDI4_DEC(256, kVF16, 8)
 #undef FDI4_DEC
   return hipErrorInvalidValue;
 }

@@ -47,6 +47,7 @@ struct DecodeArgs {
   int page_rows, pages_per_group, max_pages, hq_per_kv, num_pages;
   int chunks_per_split, num_splits, num_q_heads;
   int final_out;                        // 1: normalized output; 0: split partials
+  int waves;                            // wave64s per workgroup (4 or 8)
   float* out;
   int64_t o_b, o_h;
   float* ws_acc;                        // [B, Hq, S, D]

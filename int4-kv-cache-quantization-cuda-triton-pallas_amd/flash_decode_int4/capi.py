@@ -66,6 +66,10 @@ SIGNATURES = {
     "fdi4_decode_paged": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64,
                                   ctypes.POINTER(PagedCache), c_void_p, c_int64, c_int64, c_int,
                                   c_void_p, c_size_t, c_void_p]),
+    "fdi4_decode_partials_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "fdi4_decode_paged_partials": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64,
+                                           ctypes.POINTER(PagedCache), c_int, c_void_p,
+                                           c_size_t, c_void_p]),
     "fdi4_merge_splits": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
                                   c_int64, c_int64, c_void_p]),
     "fdi4_pack_int4": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_int64, c_int,

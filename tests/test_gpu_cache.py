@@ -1,0 +1,119 @@
+"""INT4PagedKVCache over the device page pool (reference
+tests/test_vllm_integration.py:12-101), plus exactness against the oracle."""
+
+import numpy as np
+import pytest
+
+from oracle import f64_attention, online_softmax_fp32_ref, online_softmax_ref, quantize_int4_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _cache(*a):
+    from flash_decode_int4.vllm_integration import INT4PagedKVCache
+    return INT4PagedKVCache(*a)
+
+
+class TestINT4PagedKVCache:
+
+    def test_write_and_decode(self):
+        np.random.seed(0)
+        cache = _cache(16, 128, 64)
+        for b in range(4):
+            cache.write_block(b, np.random.randn(128, 64).astype(np.float32),
+                              np.random.randn(128, 64).astype(np.float32))
+        out = cache.decode_attention(np.random.randn(2, 4, 64).astype(np.float32), [0, 1, 2, 3])
+        assert out.shape == (2, 4, 64) and np.isfinite(out).all()
+
+    def test_int4_decode_close_to_fp32(self):
+        np.random.seed(1)
+        head_dim = 64
+        cache = _cache(8, 256, head_dim)
+        keys, values = [], []
+        for b in range(3):
+            k = np.random.randn(256, head_dim).astype(np.float32)
+            v = np.random.randn(256, head_dim).astype(np.float32)
+            cache.write_block(b, k, v)
+            keys.append(k)
+            values.append(v)
+        query = (np.random.randn(1, 2, head_dim) / np.sqrt(head_dim)).astype(np.float32)
+        out = cache.decode_attention(query, [0, 1, 2])
+        ref = online_softmax_fp32_ref(query, keys, values, np.full(3, 256, dtype=np.int32))
+        assert np.abs(out - ref).mean() < 0.05
+
+    def test_matches_reference_cache_semantics(self):
+        """The reference cache quantizes each block as one group, stores V as fp16
+        and attends every query over the block table; the oracle on the same
+        (fp16-rounded) values is the exact expectation."""
+        rng = np.random.RandomState(5)
+        cache = _cache(8, 96, 48)
+        blocks = {}
+        for b, rows in [(2, 96), (5, 40), (0, 96), (7, 1)]:
+            k = rng.randn(rows, 48).astype(np.float32)
+            v = rng.randn(rows, 48).astype(np.float32)
+            cache.write_block(b, k, v)
+            blocks[b] = (k, v)
+        table = [5, 0, 7, 2]
+        query = rng.randn(2, 3, 48).astype(np.float32)
+        got = cache.decode_attention(query, table)
+        pages, vals, lens = [], [], []
+        for b in table:
+            k, v = blocks[b]
+            q_, s_, z_ = quantize_int4_ref(k)
+            pages.append((q_, s_, z_))
+            vals.append(v.astype(np.float16).astype(np.float32))
+            lens.append(len(k))
+        ref = online_softmax_ref(query, pages, vals, np.array(lens))[0]
+        f64 = f64_attention(query, [p[0] for p in pages], [p[1] for p in pages],
+                            [p[2] for p in pages], vals, lens)
+        assert np.abs(got - ref).max() < 1e-5
+        assert np.abs(got - f64).max() < 1e-5
+        np.testing.assert_array_equal(cache.k_scale[5], pages[0][1])
+
+    def test_free_block(self):
+        cache = _cache(4, 64, 32)
+        k = np.random.randn(64, 32).astype(np.float32)
+        cache.write_block(0, k, k)
+        cache.free_block(0)
+        assert 0 not in cache.k_packed
+        assert cache.memory_stats()["blocks"] == 0
+
+    def test_memory_compression_ratio(self):
+        cache = _cache(16, 256, 128)
+        for b in range(8):
+            k = np.random.randn(256, 128).astype(np.float32)
+            cache.write_block(b, k, k)
+        stats = cache.memory_stats()
+        assert stats["ratio"] > 1.5, stats
+
+    def test_packed_storage_is_real(self):
+        from oracle import pack_int4
+        np.random.seed(7)
+        cache = _cache(4, 128, 64)
+        k = np.random.randn(128, 64).astype(np.float32)
+        v = np.random.randn(128, 64).astype(np.float32)
+        cache.write_block(0, k, v)
+        assert cache.k_packed[0].nbytes == 128 * 64 // 2
+        np.testing.assert_array_equal(cache.k_packed[0], pack_int4(quantize_int4_ref(k)[0]))
+        out = cache.decode_attention((np.random.randn(1, 2, 64) / 8.0).astype(np.float32), [0])
+        assert np.isfinite(out).all()
+
+    def test_variable_block_lengths(self):
+        np.random.seed(2)
+        cache = _cache(4, 128, 32)
+        cache.write_block(0, np.random.randn(128, 32).astype(np.float32),
+                          np.random.randn(128, 32).astype(np.float32))
+        cache.write_block(1, np.random.randn(40, 32).astype(np.float32),
+                          np.random.randn(40, 32).astype(np.float32))
+        out = cache.decode_attention(np.random.randn(1, 1, 32).astype(np.float32), [0, 1])
+        assert np.isfinite(out).all()
+
+    def test_unknown_block_raises_keyerror(self):
+        cache = _cache(4, 16, 64)
+        with pytest.raises(KeyError):
+            cache.decode_attention(np.zeros((1, 1, 64), np.float32), [3])
+
+    def test_oversized_block_rejected(self):
+        cache = _cache(4, 16, 64)
+        with pytest.raises(ValueError):
+            cache.write_block(0, np.zeros((17, 64), np.float32), np.zeros((17, 64), np.float32))

@@ -1,0 +1,136 @@
+"""The C ABI called directly through ctypes with raw device pointers -- the
+path a non-torch caller (cgo, JNI, N-API, ctypes) takes -- checked against the
+oracle and against the torch binding."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import paged_decode_f64, paged_decode_ref, quantize_int4_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def test_quantize_int4_exact_reference_signature():
+    """fdi4_quantize_int4: the reference's cu_quantize_int4 argument list."""
+    import torch
+    from flash_decode_int4 import capi
+    lib = capi.load()
+    kv = np.random.RandomState(3).randn(1000, 96).astype(np.float32)
+    x = torch.from_numpy(kv).cuda()
+    q = torch.empty(1000, 96, dtype=torch.uint8, device="cuda")
+    s = torch.empty(96, device="cuda")
+    z = torch.empty(96, device="cuda")
+    capi.check(lib.fdi4_quantize_int4(_ptr(x), 1000, 96, _ptr(q), _ptr(s), _ptr(z), _stream()))
+    torch.cuda.synchronize()
+    qr, sr, zr = quantize_int4_ref(kv)
+    np.testing.assert_array_equal(q.cpu().numpy(), qr)
+    np.testing.assert_array_equal(s.cpu().numpy(), sr)
+    np.testing.assert_array_equal(z.cpu().numpy(), zr)
+
+
+def test_flash_decode_int4_exact_reference_signature():
+    """fdi4_flash_decode_int4: the reference's cu_flash_decode_int4 argument list
+    (unpacked keys, shared page stream)."""
+    import torch
+    from flash_decode_int4 import capi
+    from oracle import online_softmax_ref
+    lib = capi.load()
+    rng = np.random.RandomState(4)
+    B, H, D, nb, bs = 2, 3, 64, 3, 48
+    query = rng.randn(B, H, D).astype(np.float32)
+    kq, ss, zz, vv = [], [], [], []
+    for _ in range(nb):
+        q_, s_, z_ = quantize_int4_ref(rng.randn(bs, D).astype(np.float32))
+        kq.append(q_); ss.append(s_); zz.append(z_); vv.append(rng.randn(bs, D).astype(np.float32))
+    lens = np.array([48, 0, 31], np.int32)
+    dev = [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in
+           (query, np.stack(kq), np.stack(ss), np.stack(zz), np.stack(vv), lens)]
+    out = torch.empty(B, H, D, device="cuda")
+    capi.check(lib.fdi4_flash_decode_int4(*[_ptr(t) for t in dev], B, H, D, nb, bs, _ptr(out),
+                                          _stream()))
+    torch.cuda.synchronize()
+    ref = online_softmax_ref(query, list(zip(kq, ss, zz)), vv, lens)[0]
+    assert np.abs(out.cpu().numpy() - ref).max() < 1e-5
+
+
+def test_decode_paged_through_ctypes_matches_oracle_and_binding():
+    import torch
+    from flash_decode_int4 import capi, ops
+    from flash_decode_int4.workloads import make_workload
+    lib = capi.load()
+    w = make_workload(batch=3, heads=4, head_dim=128, seq_lens=[100, 1000, 0], seed=41)
+    dev = torch.device("cuda")
+    B, H, D = 3, 4, 128
+    G = (w["max_tokens"] + 127) // 128
+    kp = torch.zeros(w["num_pages"], H, 16, 64, dtype=torch.uint8, device=dev)
+    s = torch.zeros(B, H, G, D, device=dev)
+    z = torch.zeros(B, H, G, D, device=dev)
+    sl = torch.from_numpy(w["seq_lens"]).to(dev)
+    pt = torch.from_numpy(w["page_table"]).to(dev)
+    k = torch.from_numpy(w["k"]).to(dev)
+    v = torch.from_numpy(w["v_pages"]).to(dev)
+    q = torch.from_numpy(w["q"]).to(dev)
+    cache = capi.PagedCache(
+        k_pages=kp.data_ptr(), k_page_stride=kp.stride(0), k_head_stride=kp.stride(1),
+        k_row_stride=kp.stride(2), v_pages=v.data_ptr(), v_dtype=capi.V_F32,
+        v_page_stride=v.stride(0), v_head_stride=v.stride(1), v_row_stride=v.stride(2),
+        k_scale=s.data_ptr(), k_zp=z.data_ptr(), s_batch_stride=s.stride(0),
+        s_head_stride=s.stride(1), s_group_stride=s.stride(2), s_page_stride=0,
+        page_table=pt.data_ptr(), pt_batch_stride=pt.stride(0), seq_lens=sl.data_ptr(),
+        page_lens=None, pl_batch_stride=0, num_kv_heads=H, head_dim=D, page_rows=16,
+        pages_per_group=8, max_pages=pt.shape[1], num_pages=w["num_pages"])
+    capi.check(lib.fdi4_quantize_paged(_ptr(k), B, k.shape[2], k.stride(0), k.stride(1),
+                                       k.stride(2), 128, cache, _stream()), "quantize_paged")
+    splits = lib.fdi4_decode_num_splits(B, H, cache)
+    nbytes = lib.fdi4_decode_workspace_bytes(B, H, D, splits)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+    out = torch.empty(B, H, D, device=dev)
+    capi.check(lib.fdi4_decode_paged(_ptr(q), B, H, q.stride(0), q.stride(1), cache, _ptr(out),
+                                     out.stride(0), out.stride(1), splits, _ptr(ws), ws.numel(),
+                                     _stream()), "decode_paged")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    args = (w["q"], kp.cpu().numpy(), w["v_pages"], s.cpu().numpy(), z.cpu().numpy(),
+            w["page_table"], w["seq_lens"])
+    o32, o64 = paged_decode_ref(*args), paged_decode_f64(*args)
+    assert np.abs(got - o32).max() <= max(1e-5, 1.25 * np.abs(o32 - o64).max())
+    np.testing.assert_array_equal(got[2], 0.0)
+    via_binding = ops.flash_decode_paged(q, kp, v, s, z, pt, sl, num_splits=splits)
+    assert bool((via_binding == out).all())
+
+
+def test_partials_then_merge_equals_one_call():
+    """fdi4_decode_paged_partials + fdi4_merge_splits == fdi4_decode_paged."""
+    import torch
+    from flash_decode_int4 import ops
+    from flash_decode_int4.workloads import make_workload
+    C = ops._C
+    w = make_workload(batch=2, heads=4, head_dim=128, seq_lens=[2048, 333], seed=42)
+    dev = torch.device("cuda")
+    G = 16
+    kp = torch.zeros(w["num_pages"], 4, 16, 64, dtype=torch.uint8, device=dev)
+    s = torch.zeros(2, 4, G, 128, device=dev)
+    z = torch.zeros(2, 4, G, 128, device=dev)
+    sl = torch.from_numpy(w["seq_lens"]).to(dev)
+    pt = torch.from_numpy(w["page_table"]).to(dev)
+    ops.quantize_int4_paged(torch.from_numpy(w["k"]).to(dev), sl, pt, kp, s, z, 128)
+    q = torch.from_numpy(w["q"]).to(dev)
+    v = torch.from_numpy(w["v_pages"]).to(dev)
+    for S in (1, 4, 9):
+        parts = torch.empty(int(C.decode_partials_bytes(2, 4, 128, S)), dtype=torch.uint8,
+                            device=dev)
+        C.decode_paged_partials(q, kp, v, s, z, pt, sl, None, 8, pt.shape[1], S, parts)
+        merged = C.merge_splits(parts, 2, 4, 128, S)
+        one = ops.flash_decode_paged(q, kp, v, s, z, pt, sl, num_splits=S)
+        assert (merged - one).abs().max().item() < 1e-6, S

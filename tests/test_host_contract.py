@@ -1,0 +1,232 @@
+"""Host-side behaviour that needs no GPU: the input contract and its messages,
+backend honesty, the storage helpers, the workload byte model, and the C-ABI
+library's exported surface."""
+
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from flash_decode_int4 import int4_pack, ops, workloads
+from flash_decode_int4._validate import normalize_attention_inputs
+
+from conftest import ROOT
+
+
+def _paged_problem(batch=2, heads=3, dim=32, n_blocks=3, rows=64, seed=0):
+    rng = np.random.RandomState(seed)
+    query = (rng.randn(batch, heads, dim) / np.sqrt(dim)).astype(np.float32)
+    k_q, k_s, k_z, vals = [], [], [], []
+    for _ in range(n_blocks):
+        k = rng.randn(rows, dim).astype(np.float32)
+        v = rng.randn(rows, dim).astype(np.float32)
+        q, s_, z = oracle.quantize_int4_ref(k)
+        k_q.append(q); k_s.append(s_); k_z.append(z); vals.append(v)
+    return query, k_q, k_s, k_z, vals
+
+
+class TestAttentionInputContract:
+    """reference tests/test_ops_dispatch.py:181-243: the same ValueError messages,
+    raised before any device work (so they hold on a host without a GPU)."""
+
+    def test_block_len_longer_than_page_is_rejected(self):
+        query, k_q, k_s, k_z, vals = _paged_problem(rows=64)
+        with pytest.raises(ValueError, match="outside"):
+            ops.flash_decode(query, k_q, k_s, k_z, vals, np.array([64, 65, 64]), backend="hip")
+
+    def test_negative_block_len_is_rejected(self):
+        query, k_q, k_s, k_z, vals = _paged_problem()
+        with pytest.raises(ValueError, match="outside"):
+            ops.flash_decode(query, k_q, k_s, k_z, vals, np.array([64, -1, 64]), backend="hip")
+
+    def test_wrong_number_of_block_lens_is_rejected(self):
+        query, k_q, k_s, k_z, vals = _paged_problem()
+        with pytest.raises(ValueError, match="entries"):
+            ops.flash_decode(query, k_q, k_s, k_z, vals, np.array([64, 64]), backend="hip")
+
+    def test_mismatched_page_lists_are_rejected(self):
+        query, k_q, k_s, k_z, vals = _paged_problem()
+        with pytest.raises(ValueError, match="same length"):
+            ops.flash_decode(query, k_q, k_s, k_z, vals[:-1], backend="hip")
+
+    def test_value_page_shape_mismatch_is_rejected(self):
+        query, k_q, k_s, k_z, vals = _paged_problem()
+        vals[1] = vals[1][:-3]
+        with pytest.raises(ValueError, match="value page 1"):
+            ops.flash_decode(query, k_q, k_s, k_z, vals, backend="hip")
+
+    def test_key_page_wrong_head_dim_is_rejected(self):
+        query, k_q, k_s, k_z, vals = _paged_problem(dim=32)
+        with pytest.raises(ValueError, match="key page"):
+            ops.flash_decode(query[:, :, :16], k_q, k_s, k_z, vals, backend="hip")
+
+    def test_scale_shape_is_checked(self):
+        query, k_q, k_s, k_z, vals = _paged_problem(dim=32)
+        k_s[0] = k_s[0][:5]
+        with pytest.raises(ValueError, match="scale/zero-point"):
+            ops.flash_decode(query, k_q, k_s, k_z, vals, backend="hip")
+
+    def test_non_3d_query_is_rejected(self):
+        query, k_q, k_s, k_z, vals = _paged_problem()
+        with pytest.raises(ValueError, match="query must be"):
+            ops.flash_decode(query[0], k_q, k_s, k_z, vals, backend="hip")
+
+    def test_empty_cache_returns_exact_zeros(self):
+        query, *_ = _paged_problem()
+        out = ops.flash_decode(query, [], [], [], [], backend="hip")
+        assert out.shape == query.shape and out.dtype == np.float32
+        np.testing.assert_array_equal(out, 0.0)
+
+    def test_lens_are_int32(self):
+        query, k_q, k_s, k_z, vals = _paged_problem()
+        _, lens = normalize_attention_inputs(query, k_q, k_s, k_z, vals, [64, 10, 0])
+        assert lens.dtype == np.int32 and list(lens) == [64, 10, 0]
+        _, lens = normalize_attention_inputs(query, k_q, k_s, k_z, vals, None)
+        assert list(lens) == [64, 64, 64]
+
+
+class TestBackendHonesty:
+    """reference tests/test_ops_dispatch.py:90-139: a named backend is delivered or
+    refused, never substituted; this build has no CPU implementation."""
+
+    def test_unknown_backend(self):
+        with pytest.raises(ValueError, match="unknown backend"):
+            ops.flash_decode(*_paged_problem(), backend="nonsense")
+        with pytest.raises(ValueError, match="unknown backend"):
+            ops.quantize_int4(np.zeros((4, 4), np.float32), backend="nonsense")
+
+    @pytest.mark.parametrize("name", ["reference", "triton", "pallas"])
+    def test_backends_not_in_this_build_are_refused(self, name):
+        with pytest.raises(ValueError):
+            ops.flash_decode(*_paged_problem(), backend=name)
+        with pytest.raises(ValueError):
+            ops.quantize_int4(np.zeros((4, 4), np.float32), backend=name)
+
+    def test_declared_backends(self):
+        assert ops.QUANTIZE_BACKENDS == ("hip", "cuda")
+        assert ops.ATTENTION_BACKENDS == ("hip", "cuda")
+        assert ops.CUDA_MAX_HEAD_DIM == 256
+
+    def test_use_cuda_false_is_refused(self):
+        with pytest.raises(RuntimeError, match="CPU"):
+            ops.quantize_int4(np.zeros((4, 4), np.float32), use_cuda=False)
+
+    @pytest.mark.skipif(ops.HAS_HIP, reason="checks the no-GPU failure mode")
+    def test_no_gpu_fails_loudly(self):
+        with pytest.raises(RuntimeError):
+            ops.quantize_int4(np.zeros((4, 4), np.float32))
+        with pytest.raises(RuntimeError):
+            ops.flash_decode(*_paged_problem())
+
+    def test_backend_status(self):
+        st = ops.backend_status()
+        assert st["active_backend"] in ("hip", "unavailable")
+        assert st["has_extension"] is True
+
+
+class TestHostPacking:
+
+    @pytest.mark.parametrize("shape", [(256, 64), (10, 7), (4, 128, 32), (3, 1), (1, 2)])
+    def test_matches_oracle(self, shape):
+        q = np.random.RandomState(shape[-1]).randint(0, 16, shape).astype(np.uint8)
+        p = int4_pack.pack_int4(q)
+        np.testing.assert_array_equal(p, oracle.pack_int4(q))
+        np.testing.assert_array_equal(int4_pack.unpack_int4(p, shape[-1]), q)
+        assert int4_pack.packed_nbytes(shape) == p.nbytes
+
+    def test_known_answer(self):
+        q = np.array([[0, 15, 15, 0, 7, 8]], dtype=np.uint8)
+        np.testing.assert_array_equal(int4_pack.pack_int4(q), [[0xF0, 0x0F, 0x87]])
+
+    def test_rejects(self):
+        with pytest.raises(AssertionError):
+            int4_pack.pack_int4(np.array([[16]], dtype=np.uint8))
+        with pytest.raises(AssertionError):
+            int4_pack.pack_int4(np.array([[1]], dtype=np.int32))
+
+
+class TestWorkloads:
+
+    def test_anchor_bytes_match_the_measurement_plan(self):
+        """306,450,464 B per decode and 306,188,288 B per quantization at
+        B8 x H32 x D128 x 2048 (fp32 values, 16-token pages, 128-token groups)."""
+        lens = np.full(8, 2048)
+        assert workloads.decode_bytes(lens, 32, 128) == 306_450_464
+        assert workloads.quantize_bytes(lens, 32, 128) == 306_188_288
+
+    @pytest.mark.parametrize("t,mb", [(512, 76.81), (8192, 1225.0), (32768, 4899.3)])
+    def test_sweep_bytes(self, t, mb):
+        assert abs(workloads.decode_bytes(np.full(8, t), 32, 128) / 1e6 - mb) < 0.5
+
+    def test_cpu_workload_is_deterministic(self):
+        a = workloads.make_workload("cpu")
+        b = workloads.make_workload("cpu")
+        for key in ("q", "k", "v_pages", "page_table", "seq_lens"):
+            np.testing.assert_array_equal(a[key], b[key])
+        np.testing.assert_array_equal(a["page_table"][0], np.arange(32))
+
+    def test_page_tables_are_permutations(self):
+        lens = workloads.ragged_lengths(32, 8192, 1234)
+        assert lens[3] == 0 and lens[17] == 0 and (lens > 0).sum() == 30
+        assert (lens % 16 != 0).any()
+        table, P = workloads.page_layout(lens, 16, 1234)
+        used = np.concatenate([table[b, :(lens[b] + 15) // 16] for b in range(32)])
+        assert sorted(used.tolist()) == list(range(P))
+
+    def test_rope_preserves_pair_norms(self):
+        k = np.random.RandomState(0).randn(2, 10, 8).astype(np.float32)
+        r = workloads.rope_rotate(k)
+        n0 = k[..., :4] ** 2 + k[..., 4:] ** 2
+        n1 = r[..., :4] ** 2 + r[..., 4:] ** 2
+        np.testing.assert_allclose(n0, n1, rtol=1e-5)
+        np.testing.assert_array_equal(r[:, 0], k[:, 0])  # position 0 is unrotated
+
+
+class TestCABI:
+    """The C-ABI library loads on a host without a GPU and exports every
+    function include/fdi4.h declares; size queries and argument rejection run
+    without touching a device."""
+
+    def _declared(self):
+        text = open(os.path.join(ROOT, "include", "fdi4.h")).read()
+        return sorted(set(re.findall(r"\b(fdi4_[a-z0-9_]+)\s*\(", text)))
+
+    def test_every_declared_symbol_is_exported(self):
+        from flash_decode_int4 import capi
+        lib = capi.load()
+        declared = self._declared()
+        assert len(declared) >= 15
+        for name in declared:
+            assert hasattr(lib, name), name
+        assert set(declared) == set(capi.SIGNATURES), "ctypes table and header disagree"
+
+    def test_size_queries(self):
+        from flash_decode_int4 import capi
+        lib = capi.load()
+        assert lib.fdi4_abi_version() == 1
+        assert lib.fdi4_quantize_rows_workspace_bytes(512, 128) == (2 * 128 + 128) * 8
+        assert lib.fdi4_decode_workspace_bytes(8, 32, 128, 1) == 0
+        n = 8 * 32 * 4
+        assert lib.fdi4_decode_workspace_bytes(8, 32, 128, 4) == n * 128 * 4 + n * 16
+        assert lib.fdi4_decode_partials_bytes(8, 32, 128, 1) == 8 * 32 * (512 + 16)
+        # B8 x H32 fills the chip with 8-wave workgroups: one split, no merge.
+        cache = capi.PagedCache(max_pages=128, page_rows=16)
+        assert lib.fdi4_decode_num_splits(8, 32, cache) == 1
+        # B1 x H8 x 32768 tokens: 2048 chunks split 32 ways (2048 waves).
+        cache = capi.PagedCache(max_pages=2048, page_rows=16)
+        assert lib.fdi4_decode_num_splits(1, 8, cache) == 32
+
+    def test_invalid_arguments_are_rejected_before_any_device_call(self):
+        from flash_decode_int4 import capi
+        lib = capi.load()
+        bad = 1  # hipErrorInvalidValue
+        assert lib.fdi4_quantize_rows(None, 4, 4, 4, None, 4, 0, None, None, None, 0, None) == bad
+        assert lib.fdi4_decode_paged(None, 1, 1, 0, 0, None, None, 0, 0, 0, None, 0, None) == bad
+        cache = capi.PagedCache(head_dim=96, page_rows=16, num_kv_heads=1, pages_per_group=1,
+                                max_pages=1, num_pages=1, k_pages=16, k_scale=16, k_zp=16)
+        assert lib.fdi4_quantize_paged(16, 1, 16, 0, 0, 128, 128, cache, None) == bad
+        assert lib.fdi4_merge_splits(None, None, 1, 1, 128, 1, None, 0, 0, None) == bad
+        assert lib.fdi4_flash_decode_int4_ws(None, None, None, None, None, None, 1, 1, 300, 1, 1,
+                                             None, None, 0, None) == bad
