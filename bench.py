@@ -5,12 +5,13 @@ Metric: fused INT4 decode attention time (us) and its fraction of the HBM
 roofline at B8 x H32 x D128 x 2048 tokens (16-token pages, 128-token scale
 groups, fp32 values), plus the grouped quantizer's GB/s.
 
-A step is one decode of the whole batch: the split-K decode kernel plus the
-split merge, on inputs already resident in HBM. Input sets are rotated so
-their total exceeds twice the 256 MB Infinity Cache (nothing is served from
-the cache across steps). The quantizer is timed in its own loop over the same
-rotation. HIP events on the launch stream time each kernel; wall clock times
-the K steps. Bytes are algorithmic (valid tokens only): packed K T*D/2, V
+A step is one decode of the whole batch on inputs already resident in HBM:
+the decode kernel (plus the split merge when the library splits the
+sequences). Input sets are rotated so their total exceeds twice the 256 MB
+Infinity Cache (nothing is served from the cache across steps). The quantizer
+is timed in its own loop over the same rotation. One pair of HIP events on the
+launch stream brackets K back-to-back launches (per-launch markers would add
+their own time to the GPU timeline); wall clock brackets the K steps too. Bytes are algorithmic (valid tokens only): packed K T*D/2, V
 T*D*4, scale and zero-point ceil(T/128)*D*8 per (sequence, head), the page
 table, sequence lengths, q and the output.
 
@@ -110,43 +111,50 @@ def time_decode(sets, splits, steps, warmup):
     parts = torch.empty(int(C.decode_partials_bytes(B, H, D, S)), dtype=torch.uint8,
                         device="cuda")
 
-    def step(i, ev=None):
+    def step(i):
         # The production call: with one split it is the decode kernel alone
         # (writing the output); with several it is the decode kernel and the
-        # merge, issued here as the same two launches so each can be timed.
+        # merge -- issued here as the same two launches the one-call entry
+        # point makes, so the decode kernel can also be timed alone.
         st = sets[i % len(sets)]
-        if ev is not None:
-            ev[0].record()
         if S == 1:
-            out = C.decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
-                                 st["sl"], None, ppg, maxp, 1)
-            if ev is not None:
-                ev[1].record()
-                ev[2].record()
-            return out
+            return C.decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
+                                  st["sl"], None, ppg, maxp, 1)
         C.decode_paged_partials(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
                                 st["sl"], None, ppg, maxp, S, parts)
-        if ev is not None:
-            ev[1].record()
-        out = C.merge_splits(parts, B, H, D, S)
-        if ev is not None:
-            ev[2].record()
-        return out
+        return C.merge_splits(parts, B, H, D, S)
+
+    def decode_only(i):
+        st = sets[i % len(sets)]
+        C.decode_paged_partials(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
+                                st["sl"], None, ppg, maxp, S, parts)
+
+    def timed(fn, n):
+        """n back-to-back launches; one event pair on the launch stream (per-launch
+        event markers would add their own time to the GPU timeline) plus wall clock."""
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        out = None
+        for i in range(n):
+            out = fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return out, time.perf_counter() - t0, e0.elapsed_time(e1) * 1e3 / n
 
     for i in range(warmup):
         step(i)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        out = step(i, evs[i])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    dec = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
-    mrg = [e[1].elapsed_time(e[2]) * 1e3 for e in evs]
-    tot = [e[0].elapsed_time(e[2]) * 1e3 for e in evs]
-    return dict(splits=S, wall_s=wall, decode_us=dec, merge_us=mrg, step_us=tot,
-                last_out=out, last_set=(steps - 1) % len(sets))
+    out, wall, step_us = timed(step, steps)
+    if S == 1:
+        dec_us = step_us
+    else:
+        for i in range(warmup):
+            decode_only(i)
+        _, _, dec_us = timed(decode_only, steps)
+    return dict(splits=S, wall_s=wall, step_us=step_us, decode_us=dec_us,
+                merge_us=max(step_us - dec_us, 0.0), last_out=out,
+                last_set=(steps - 1) % len(sets))
 
 
 def time_quantizer(sets, steps, warmup):
@@ -160,15 +168,14 @@ def time_quantizer(sets, steps, warmup):
 
     for i in range(warmup):
         q(i)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    e0.record()
     for i in range(steps):
-        evs[i][0].record()
         q(i)
-        evs[i][1].record()
+    e1.record()
     torch.cuda.synchronize()
-    return [a.elapsed_time(b) * 1e3 for a, b in evs]
+    return e0.elapsed_time(e1) * 1e3 / steps
 
 
 def median(x):
@@ -345,11 +352,9 @@ def main():
 
     res = time_decode(sets, args.splits, args.steps, args.warmup)
     qt = time_quantizer(sets, args.steps, args.warmup)
-    dec_us = sum(res["decode_us"]) / len(res["decode_us"])
-    mrg_us = sum(res["merge_us"]) / len(res["merge_us"])
-    step_us = sum(res["step_us"]) / len(res["step_us"])
+    dec_us, mrg_us, step_us = res["decode_us"], res["merge_us"], res["step_us"]
     ms_per_step = res["wall_s"] / args.steps * 1e3
-    q_us = sum(qt) / len(qt)
+    q_us = qt
 
     line = {
         "metric": METRIC,
@@ -377,7 +382,6 @@ def main():
         "decode_us": round(step_us, 3),
         "decode_kernel_us": round(dec_us, 3),
         "merge_us": round(mrg_us, 3),
-        "decode_us_median": round(median(res["step_us"]), 3),
         "hbm_frac": round(set_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "quantizer_us": round(q_us, 3),
         "quantizer_gbs": round(qbytes / (q_us * 1e-6) / 1e9, 2),
