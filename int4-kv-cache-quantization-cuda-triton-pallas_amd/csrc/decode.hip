@@ -63,11 +63,11 @@ template <int KW>
 __device__ __forceinline__ KVec<KW> load_k(const uint8_t* p) {
   KVec<KW> r;
   if constexpr (KW == 4) {
-    const U32x4 v = ld16(p);
+    const U32x4 v = ld16_stream(p);
     r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
   } else {
     static_assert(KW == 2, "KW");
-    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    const uint2 v = ld8_stream(p);
     r.w[0] = v.x; r.w[1] = v.y;
   }
   return r;
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < G::VLD; ++i) {
       const int r = max(min(i * G::RPL + vrow, m.nval - 1), 0);
-      vr[i] = ld16(vb + (int64_t)r * vrow_b);
+      vr[i] = ld16_stream(vb + (int64_t)r * vrow_b);
     }
   };
 
@@ -221,9 +221,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
 
     const bool last = c + 1 >= wc1;
     // Unconditional loads: a conditional load here makes the wait counts at
-    // the loop back-edge conservative (a full drain of the prefetch).
-    load_sz(nm, sz);
-    load_chunk(nm, nk, nv);
+    // the loop back-edge conservative (a full drain of the prefetch). On the
+    // last step nm is the current chunk; with one valid row every lane reads
+    // that chunk's first row, so the dummy prefetch costs one row, not a page.
+    ChunkMeta pf = nm;
+    pf.nval = last ? 1 : nm.nval;
+    load_sz(pf, sz);
+    load_chunk(pf, nk, nv);
     const ChunkMeta nnm = meta_at(c + 2);
     if (cm.nval > 0) {
 

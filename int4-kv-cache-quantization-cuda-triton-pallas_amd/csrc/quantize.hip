@@ -184,7 +184,7 @@ __global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArg
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int r = rsub + i * RPI;
-    if (r < nrows) x[i] = *reinterpret_cast<const float4*>(src + (int64_t)r * a.k_t);
+    if (r < nrows) x[i] = ld16f_stream(src + (int64_t)r * a.k_t);
   }
 
   float mn[4], mx[4];
