@@ -19,9 +19,13 @@ The cpu_baseline leg times the NumPy oracle (the reference's page loop, one
 call per (sequence, head) stream, one BLAS thread) on this host's cores over
 the same workload and uses its output as the parity check of the GPU result.
 
+The HBM traffic of the decode kernel comes from two rocprofv3 --pmc child
+runs (FETCH_SIZE, then WRITE_SIZE), each calibrated by the same counter on a
+256 MiB elementwise kernel; --no-pmc skips them (and must be given when this
+script itself runs under rocprofv3).
+
 Prints ONE JSON line. Options: --workload (anchor, sweep_512 ... llama,
-ragged), --splits, --value-dtype float16, --no-cpu, --pmc (HBM traffic of the
-decode kernel from two rocprofv3 --pmc child runs).
+ragged), --splits, --value-dtype float16, --no-cpu, --no-pmc.
 """
 
 import argparse
@@ -55,8 +59,8 @@ def parse():
     p.add_argument("--value-dtype", default="float32", choices=["float32", "float16"])
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     p.add_argument("--cpu-runs", type=int, default=3)
-    p.add_argument("--pmc", action="store_true",
-                   help="measure HBM traffic per decode launch with rocprofv3 --pmc")
+    p.add_argument("--no-pmc", action="store_true",
+                   help="skip the rocprofv3 --pmc traffic runs (required under rocprofv3)")
     p.add_argument("--pmc-child", default="", help=argparse.SUPPRESS)
     return p.parse_args()
 
@@ -396,7 +400,7 @@ def main():
             "kernel": f"decode_kernel<D={w0['head_dim']}, {args.value_dtype} values>",
         },
     }
-    if args.pmc:
+    if not args.no_pmc:
         traffic, err = pmc_traffic(args)
         if traffic is not None:
             line["roofline"]["traffic"] = round(traffic["fetch_bytes"] + traffic["write_bytes"])

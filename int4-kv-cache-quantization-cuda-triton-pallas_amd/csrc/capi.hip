@@ -47,10 +47,14 @@ int env_int(const char* name, int dflt) {
   return x > 0 ? x : dflt;
 }
 
+// Eight waves as soon as each gets kMinChunksPerWave chunks: more waves per
+// workgroup merge in LDS, where more splits need the merge kernel (at B8 H32
+// T512, 8 waves and one split take 16.5 us against 19.2 us for 4 waves, two
+// splits and the merge).
 int pick_waves(int chunks) {
   const int w = env_int("FDI4_DECODE_WAVES", 0);
   if (w == 4 || w == 8) return w;
-  return chunks >= 8 * 2 * kMinChunksPerWave ? 8 : 4;
+  return chunks >= 8 * kMinChunksPerWave ? 8 : 4;
 }
 
 int auto_splits(int batch, int hq, int chunks) {

@@ -139,6 +139,16 @@ __device__ __forceinline__ uint2 ld8_stream(const void* p) {
   return r;
 }
 
+// Non-temporal 16-byte store for output written once and not read back by
+// the same kernel.
+__device__ __forceinline__ void st16_stream(void* p, U32x4 v) {
+  U32x4* q = reinterpret_cast<U32x4*>(p);
+  __builtin_nontemporal_store(v.x, &q->x);
+  __builtin_nontemporal_store(v.y, &q->y);
+  __builtin_nontemporal_store(v.z, &q->z);
+  __builtin_nontemporal_store(v.w, &q->w);
+}
+
 __device__ __forceinline__ float4 ld16f_stream(const float* p) {
   const float4* q = reinterpret_cast<const float4*>(p);
   float4 r;

@@ -214,6 +214,9 @@ class TestCABI:
         # B8 x H32 fills the chip with 8-wave workgroups: one split, no merge.
         cache = capi.PagedCache(max_pages=128, page_rows=16)
         assert lib.fdi4_decode_num_splits(8, 32, cache) == 1
+        # T=512 (32 chunks): still 8 waves of 4 chunks and one split.
+        cache = capi.PagedCache(max_pages=32, page_rows=16)
+        assert lib.fdi4_decode_num_splits(8, 32, cache) == 1
         # B1 x H8 x 32768 tokens: 2048 chunks split 32 ways (2048 waves).
         cache = capi.PagedCache(max_pages=2048, page_rows=16)
         assert lib.fdi4_decode_num_splits(1, 8, cache) == 32
