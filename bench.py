@@ -65,12 +65,14 @@ def parse():
     return p.parse_args()
 
 
-def build_sets(name, value_dtype, n_sets_hint=0):
-    """Independent input sets in HBM (different seeds), keys quantized into pages."""
+def build_sets(name, value_dtype, n_sets_hint=0, seq_lens=None):
+    """Independent input sets in HBM (different seeds), keys quantized into pages.
+    seq_lens overrides the workload's lengths (same heads, head_dim and pages)."""
     import torch
     from flash_decode_int4 import ops, workloads
     sets = []
-    first = workloads.make_workload(name, value_dtype=value_dtype, backend="torch", seed=1234)
+    first = workloads.make_workload(name, seq_lens=seq_lens, value_dtype=value_dtype,
+                                    backend="torch", seed=1234)
     vbytes = 2 if value_dtype == "float16" else 4
     set_bytes = workloads.decode_bytes(first["seq_lens"], first["heads"], first["head_dim"],
                                        vbytes)
@@ -261,11 +263,13 @@ def cpu_baseline(st, gpu_out, runs, vbytes):
 
 
 def pmc_child(args):
-    """Run a few decode launches on one set (for rocprofv3 --pmc); also a
-    256 MiB device copy whose counters calibrate the bytes/counter factor."""
+    """Run a few decode and quantizer launches on one set (for rocprofv3
+    --pmc); also a 256 MiB device copy whose counters calibrate the
+    bytes/counter factor."""
     import torch
     sets, _ = build_sets(args.workload, args.value_dtype, n_sets_hint=1)
     r = time_decode(sets, args.splits, steps=3, warmup=1)
+    time_quantizer(sets, steps=3, warmup=1)
     a = torch.empty(64 * 2 ** 20, dtype=torch.float32, device="cuda")
     b = torch.empty_like(a)
     a.fill_(1.0)
@@ -356,6 +360,15 @@ def main():
 
     res = time_decode(sets, args.splits, args.steps, args.warmup)
     qt = time_quantizer(sets, args.steps, args.warmup)
+
+    # No shape specialization (the reference bench re-runs at seq_len + 1): every
+    # length + 1, so pages end one row into a fresh page and groups one row into
+    # a fresh group; the output must be finite and the rate must hold.
+    odd_lens = w0["seq_lens"] + 1
+    odd_sets, odd_bytes = build_sets(args.workload, args.value_dtype, seq_lens=odd_lens)
+    odd = time_decode(odd_sets, args.splits, max(args.steps // 2, 5), args.warmup)
+    odd_ok = bool(torch.isfinite(odd["last_out"]).all())
+    del odd_sets
     dec_us, mrg_us, step_us = res["decode_us"], res["merge_us"], res["step_us"]
     ms_per_step = res["wall_s"] / args.steps * 1e3
     q_us = qt
@@ -390,6 +403,13 @@ def main():
         "quantizer_us": round(q_us, 3),
         "quantizer_gbs": round(qbytes / (q_us * 1e-6) / 1e9, 2),
         "quantizer_hbm_frac": round(qbytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "checks": {
+            "split_invariance_max_abs": gate,
+            "seq_len_plus_1": {
+                "pass": odd_ok, "max_tokens": int(odd_lens.max()),
+                "decode_us": round(odd["step_us"], 3),
+                "hbm_frac": round(odd_bytes / (odd["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+        },
         "roofline": {
             "bound": "hbm",
             "achieved": round(set_bytes / (dec_us * 1e-6) / 1e9, 2),

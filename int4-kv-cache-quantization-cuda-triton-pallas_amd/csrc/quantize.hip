@@ -8,7 +8,10 @@
 //   zp     = (-mn) / scale                (IEEE division)
 //   q      = clamp(rintf((x - mn) / scale), 0, 15)   (round half to even)
 // This file is compiled with -ffp-contract=off and without fast-math so that
-// every operation above is one correctly rounded float32 operation.
+// every operation above is one correctly rounded float32 operation. The
+// grouped kernel forms the quotient (x - mn) / scale from the channel's
+// reciprocal with one FMA correction step (quant_bin_rc), which returns the
+// same correctly rounded quotient for a third of the instructions.
 //
 // Kernels
 //   rows_minmax_kernel / rows_finalize_kernel / rows_quantize_kernel
@@ -17,9 +20,9 @@
 //       that any row count fills the chip; unpacked or nibble-packed output.
 //   quantize_paged_kernel<D, GROUP>
 //       one workgroup per (group, kv-head, sequence): 16-byte token-major
-//       loads held in registers, wave64 min/max reduction, quantize from
-//       registers, nibble pack, and 16-byte stores of whole page rows through
-//       the page table.
+//       non-temporal loads held in registers, wave64 min/max reduction,
+//       quantize from registers, nibble pack, and 16-byte non-temporal stores
+//       of whole page rows through the page table.
 //   pack_kernel   device form of the nibble packing (reference src/int4_pack.py:14-29)
 
 #include "fdi4_device.hpp"
@@ -31,6 +34,20 @@ __device__ __forceinline__ unsigned quant_bin(float x, float mn, float scale) {
   float b = rintf((x - mn) / scale);
   b = fminf(fmaxf(b, 0.0f), 15.0f);
   return (unsigned)b;
+}
+
+// The same bin with the division done from the reciprocal rc = 1.0f / scale
+// (one IEEE division per channel): q0 = y * rc, then one FMA residual step
+// q = fma(fma(-q0, scale, y), rc, q0) yields the correctly rounded quotient
+// RN(y / scale) (Markstein's correction: rc is the correctly rounded
+// reciprocal, the residual y - q0 * scale is exact under FMA, and no
+// intermediate under- or overflows for 0 <= y <= span and scale >= 1e-8/15).
+// Infinite or NaN inputs give a NaN quotient and bin 0, as the division does.
+__device__ __forceinline__ float quant_bin_rc(float x, float mn, float scale, float rc) {
+  const float y = x - mn;
+  const float q0 = y * rc;
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, scale, y), rc, q0);
+  return fminf(fmaxf(rintf(q), 0.0f), 15.0f);
 }
 
 __device__ __forceinline__ void scale_zp(float mn, float mx, float* s, float* z) {
@@ -180,11 +197,14 @@ __global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArg
   const int cq = tid % VPR, rsub = tid / VPR;
 
   const float* src = a.k + (int64_t)b * a.k_b + (int64_t)h * a.k_h + (int64_t)r0 * a.k_t + 4 * cq;
+  // Rows past the valid count load the last valid row again (same lines, no
+  // extra HBM traffic): every register holds a valid value, and duplicates
+  // change neither the minimum nor the maximum.
   float4 x[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const int r = rsub + i * RPI;
-    if (r < nrows) x[i] = ld16f_stream(src + (int64_t)r * a.k_t);
+    const int r = min(rsub + i * RPI, nrows - 1);
+    x[i] = ld16f_stream(src + (int64_t)r * a.k_t);
   }
 
   float mn[4], mx[4];
@@ -195,12 +215,10 @@ __global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArg
   }
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    if (rsub + i * RPI < nrows) {
-      mn[0] = fminf(mn[0], x[i].x); mx[0] = fmaxf(mx[0], x[i].x);
-      mn[1] = fminf(mn[1], x[i].y); mx[1] = fmaxf(mx[1], x[i].y);
-      mn[2] = fminf(mn[2], x[i].z); mx[2] = fmaxf(mx[2], x[i].z);
-      mn[3] = fminf(mn[3], x[i].w); mx[3] = fmaxf(mx[3], x[i].w);
-    }
+    mn[0] = fminf(mn[0], x[i].x); mx[0] = fmaxf(mx[0], x[i].x);
+    mn[1] = fminf(mn[1], x[i].y); mx[1] = fmaxf(mx[1], x[i].y);
+    mn[2] = fminf(mn[2], x[i].z); mx[2] = fmaxf(mx[2], x[i].z);
+    mn[3] = fminf(mn[3], x[i].w); mx[3] = fmaxf(mx[3], x[i].w);
   }
   // Lanes of one wave that own the same channels differ in the bits >= VPR.
 #pragma unroll
@@ -233,15 +251,21 @@ __global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArg
 
   // Quantize from registers; two bytes (channels 4cq..4cq+3) per owned row.
   __shared__ uint16_t s_out[GROUP * RB / 2];
+  float rc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) rc[k] = 1.0f / sc[k];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int r = rsub + i * RPI;
     if (r < nrows) {
-      const unsigned n0 = quant_bin(x[i].x, mn[0], sc[0]);
-      const unsigned n1 = quant_bin(x[i].y, mn[1], sc[1]);
-      const unsigned n2 = quant_bin(x[i].z, mn[2], sc[2]);
-      const unsigned n3 = quant_bin(x[i].w, mn[3], sc[3]);
-      s_out[r * (RB / 2) + cq] = (uint16_t)(n0 | (n1 << 4) | (n2 << 8) | (n3 << 12));
+      const float n0 = quant_bin_rc(x[i].x, mn[0], sc[0], rc[0]);
+      const float n1 = quant_bin_rc(x[i].y, mn[1], sc[1], rc[1]);
+      const float n2 = quant_bin_rc(x[i].z, mn[2], sc[2], rc[2]);
+      const float n3 = quant_bin_rc(x[i].w, mn[3], sc[3], rc[3]);
+      // n0 | n1 << 4 | n2 << 8 | n3 << 12 in exact float arithmetic (< 2^16).
+      const float pk = __builtin_fmaf(
+          n3, 4096.0f, __builtin_fmaf(n2, 256.0f, __builtin_fmaf(n1, 16.0f, n0)));
+      s_out[r * (RB / 2) + cq] = (uint16_t)(unsigned)pk;
     }
   }
   __syncthreads();

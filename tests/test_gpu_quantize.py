@@ -149,3 +149,71 @@ class TestPagedQuantizer:
                 n = min(16, 300 - lp * 16)
                 np.testing.assert_array_equal(kpn[w["page_table"][b, lp], :, :n],
                                               pack_int4(qr[b, :, lp * 16:lp * 16 + n]))
+
+
+def _tie_keys(B, H, T, D, seed):
+    """Keys whose quotients (x - mn) / scale sit on or within a few ulps of
+    half-integers, per 128-row group and channel: row 0 is the minimum, row 1
+    the maximum, the other rows mn + (j + 1/2) * scale nudged by -3..3 ulps.
+    A quarter of the channels have mn = 0 and span 15 * 2^e, so the scale is a
+    power of two and the nudge-0 rows are exact ties (round half to even)."""
+    rng = np.random.RandomState(seed)
+    k = np.empty((B, H, T, D), np.float32)
+    for b in range(B):
+        for h in range(H):
+            for g0 in range(0, T, 128):
+                n = min(128, T - g0)
+                for c in range(D):
+                    if c % 4 == 0:
+                        e = rng.randint(-20, 10)
+                        mn = np.float32(0.0)
+                        mx = np.float32(15.0 * 2.0 ** e)
+                    else:
+                        span = 10.0 ** rng.uniform(-6, 3)
+                        mn = np.float32(rng.uniform(-2, 2) * span)
+                        mx = np.float32(mn + np.float32(span))
+                    s = np.float32(np.maximum(np.float32(mx - mn), np.float32(1e-8)) /
+                                   np.float32(15.0))
+                    col = np.empty(n, np.float32)
+                    col[0], col[1 % n] = mn, mx
+                    for r in range(2, n):
+                        j = rng.randint(0, 15)
+                        x = np.float32(np.float64(mn) + (j + 0.5) * np.float64(s))
+                        d = rng.randint(-3, 4)
+                        for _ in range(abs(d)):
+                            x = np.nextafter(x, np.float32(np.inf if d > 0 else -np.inf))
+                        col[r] = np.clip(x, mn, mx)
+                    k[b, h, g0:g0 + n, c] = col
+    return k
+
+
+class TestQuantizerTies:
+    """The grouped kernel divides through the reciprocal with an FMA correction;
+    the bins must still equal IEEE division + round-half-even at and next to
+    every tie (random data almost never lands there)."""
+
+    def test_paged_bins_at_and_near_ties(self):
+        import torch
+        from flash_decode_int4.workloads import page_layout
+        B, H, T, D = 2, 2, 300, 128
+        k = _tie_keys(B, H, T, D, seed=5)
+        lens = np.array([300, 173], np.int32)
+        table, P = page_layout(lens, 16, 5)
+        dev = torch.device("cuda")
+        kp = torch.zeros(P, H, 16, D // 2, dtype=torch.uint8, device=dev)
+        s = torch.zeros(B, H, 3, D, device=dev)
+        z = torch.zeros(B, H, 3, D, device=dev)
+        _ops().quantize_int4_paged(torch.from_numpy(k).to(dev), torch.from_numpy(lens).to(dev),
+                                   torch.from_numpy(table).to(dev), kp, s, z, 128)
+        qr, sr, zr = quantize_groups_ref(k, lens)
+        # The construction does put values on exact ties.
+        y = k[:, :, :128] - k[:, :, :1]
+        assert np.any(np.float32(y / sr[:, :, :1]) % 1 == 0.5)
+        kpn, sn = kp.cpu().numpy(), s.cpu().numpy()
+        for b in range(B):
+            ng = (lens[b] + 127) // 128
+            np.testing.assert_array_equal(sn[b, :, :ng], sr[b, :, :ng])
+            for lp in range((lens[b] + 15) // 16):
+                n = min(16, lens[b] - lp * 16)
+                np.testing.assert_array_equal(kpn[table[b, lp], :, :n],
+                                              pack_int4(qr[b, :, lp * 16:lp * 16 + n]))
