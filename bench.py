@@ -15,6 +15,10 @@ their own time to the GPU timeline); wall clock brackets the K steps too. Bytes 
 T*D*4, scale and zero-point ceil(T/128)*D*8 per (sequence, head), the page
 table, sequence lengths, q and the output.
 
+append_us times the decode-time append kernel (one token per (sequence,
+kv-head), open scale group re-quantized) on a cache of the workload's shape,
+at the first and at the last row of a group.
+
 The cpu_baseline leg times the NumPy oracle (the reference's page loop, one
 call per (sequence, head) stream, one BLAS thread) on this host's cores over
 the same workload and uses its output as the parity check of the GPU result.
@@ -182,6 +186,51 @@ def time_quantizer(sets, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / steps
+
+
+def time_append(w, value_dtype, steps, warmup):
+    """Decode-time append (one token per (sequence, kv-head)) on a cache of the
+    workload's shape: the kernel re-quantizes the open scale group, so its cost
+    runs from one row (first token of a group) to a full group (last token).
+    Both ends are timed over back-to-back launches at a fixed position (the
+    call is idempotent when the lengths are not advanced)."""
+    import torch
+    from flash_decode_int4._lib import load_binding
+    from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
+    C = load_binding()
+    B, H, D, G = w["batch"], w["heads"], w["head_dim"], w["group_rows"]
+    T = int(max(w["seq_lens"]))
+    T = max(T, G)
+    out = {}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    vdt = torch.float16 if value_dtype == "float16" else torch.float32
+    k = torch.randn(B, H, T, D, generator=g, device="cuda")
+    v = torch.randn(B, H, T, D, generator=g, device="cuda").to(vdt)
+    kn = torch.randn(B, H, D, generator=g, device="cuda")
+    vn = torch.randn(B, H, D, generator=g, device="cuda").to(vdt)
+    for name, t in (("first_row", T - G), ("full_group", T - 1)):
+        cache = INT4PagedSequenceCache(num_pages=B * (T // 16 + 2), num_kv_heads=H, head_dim=D,
+                                       max_seqs=B, max_seq_len=T, group_rows=G,
+                                       value_dtype=value_dtype)
+        cache.prefill(k, v, [t] * B)
+
+        def call():
+            C.append_paged(kn, vn, cache.k_stage, cache.k_pages, cache.v_pages, cache.k_scale,
+                           cache.k_zp, cache.page_table, cache.seq_lens, G)
+
+        for _ in range(warmup):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(e0.elapsed_time(e1) * 1e3 / steps, 3)
+        del cache
+    return out
 
 
 def median(x):
@@ -360,6 +409,7 @@ def main():
 
     res = time_decode(sets, args.splits, args.steps, args.warmup)
     qt = time_quantizer(sets, args.steps, args.warmup)
+    app = time_append(w0, args.value_dtype, args.steps, args.warmup)
 
     # No shape specialization (the reference bench re-runs at seq_len + 1): every
     # length + 1, so pages end one row into a fresh page and groups one row into
@@ -403,6 +453,7 @@ def main():
         "quantizer_us": round(q_us, 3),
         "quantizer_gbs": round(qbytes / (q_us * 1e-6) / 1e9, 2),
         "quantizer_hbm_frac": round(qbytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "append_us": app,
         "checks": {
             "split_invariance_max_abs": gate,
             "seq_len_plus_1": {

@@ -114,6 +114,26 @@ int fdi4_quantize_paged(const float* k, int batch, int max_tokens, int64_t k_bat
                         int64_t k_head_stride, int64_t k_row_stride, int group_rows,
                         const fdi4_paged_cache* cache, hipStream_t stream);
 
+/* Decode-time append of one token per sequence b < batch at position
+ * t = cache->seq_lens[b] (t < max_pages * page_rows; the caller has mapped
+ * the page holding t in cache->page_table and advances seq_lens afterwards):
+ * the value row v_new[b, h, :] (the cache's value type, element strides) goes
+ * to its page, the key row k_new[b, h, :] (float32) to row t % group_rows of
+ * k_stage[b, h, :, :] (float32, element strides), and the open scale group
+ * g = t / group_rows is re-quantized over its t % group_rows + 1 valid rows
+ * from k_stage -- packed rows to the pages, scale and zero-point to group g.
+ * The result equals fdi4_quantize_paged over the whole sequence of t + 1
+ * tokens (the reference quantizes a partial group over its valid rows,
+ * tests/test_perplexity_harness.py:122-131). k_stage must hold the open
+ * group's earlier key rows (after a prefill: rows g*group_rows .. t-1). The
+ * device form of the cache write (reference src/vllm_integration.py:48-56)
+ * for one token per step. */
+int fdi4_append_paged(const float* k_new, int64_t kn_batch_stride, int64_t kn_head_stride,
+                      const void* v_new, int64_t vn_batch_stride, int64_t vn_head_stride,
+                      int batch, float* k_stage, int64_t st_batch_stride, int64_t st_head_stride,
+                      int64_t st_row_stride, int group_rows, const fdi4_paged_cache* cache,
+                      hipStream_t stream);
+
 /* Fused INT4 flash decoding with the reference's exact arguments: query
  * [B, H, D], k_q [nb, bs, D] one INT4 value per byte, k_scale/k_zp [nb, D],
  * value [nb, bs, D] fp32, block_lens [nb]; every (b, h) query attends the same

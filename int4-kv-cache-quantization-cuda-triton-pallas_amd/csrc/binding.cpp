@@ -260,6 +260,43 @@ void quantize_paged(torch::Tensor k, torch::Tensor seq_lens, torch::Tensor page_
            "quantize_paged");
 }
 
+// One token per sequence appended at seq_lens[b] (see fdi4_append_paged);
+// seq_lens is left for the caller to advance.
+void append_paged(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_stage,
+                  torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor k_scale,
+                  torch::Tensor k_zp, torch::Tensor page_table, torch::Tensor seq_lens,
+                  int64_t group_rows) {
+  CHECK_DEV(k_new);
+  CHECK_DEV(v_new);
+  CHECK_DEV(k_stage);
+  TORCH_CHECK(k_new.scalar_type() == torch::kFloat32 && k_new.dim() == 3 && k_new.stride(2) == 1,
+              "k_new must be float32 [batch, kv_heads, head_dim] with contiguous rows");
+  TORCH_CHECK(v_new.scalar_type() == v_pages.scalar_type() && v_new.dim() == 3 &&
+                  v_new.stride(2) == 1 && v_new.sizes() == k_new.sizes(),
+              "v_new must be [batch, kv_heads, head_dim] in the cache's value dtype");
+  TORCH_CHECK(k_stage.scalar_type() == torch::kFloat32 && k_stage.dim() == 4 &&
+                  k_stage.stride(3) == 1 && k_stage.size(2) >= group_rows,
+              "k_stage must be float32 [batch, kv_heads, >= group_rows, head_dim]");
+  TORCH_CHECK(k_new.size(1) == k_pages.size(1) && k_new.size(2) == k_pages.size(3) * 2 &&
+                  k_stage.size(1) == k_pages.size(1) && k_stage.size(3) == k_new.size(2),
+              "k_new / k_stage heads and head_dim must match the cache");
+  const int64_t B = k_new.size(0);
+  TORCH_CHECK(k_stage.size(0) >= B && seq_lens.size(0) >= B && page_table.size(0) >= B &&
+                  k_scale.dim() == 4 && k_scale.size(0) >= B,
+              "k_stage, seq_lens, page_table and k_scale need a row per sequence");
+  TORCH_CHECK(group_rows % k_pages.size(2) == 0, "group_rows must be a multiple of page_rows");
+  const int64_t max_pages = page_table.size(1);
+  TORCH_CHECK(k_scale.size(2) * (group_rows / k_pages.size(2)) >= max_pages,
+              "k_scale has fewer than ceil(max_pages / pages_per_group) groups");
+  fdi4_paged_cache c = make_cache(k_pages, &v_pages, k_scale, k_zp, page_table, seq_lens,
+                                  c10::nullopt, group_rows / k_pages.size(2), max_pages);
+  check_rc(fdi4_append_paged(k_new.data_ptr<float>(), k_new.stride(0), k_new.stride(1),
+                             v_new.data_ptr(), v_new.stride(0), v_new.stride(1), (int)B,
+                             k_stage.data_ptr<float>(), k_stage.stride(0), k_stage.stride(1),
+                             k_stage.stride(2), (int)group_rows, &c, stream()),
+           "append_paged");
+}
+
 torch::Tensor decode_paged(torch::Tensor query, torch::Tensor k_pages, torch::Tensor v_pages,
                            torch::Tensor k_scale, torch::Tensor k_zp,
                            c10::optional<torch::Tensor> page_table,
@@ -392,6 +429,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Fused online softmax + INT4 dequant attention over a shared page stream (HIP)");
   m.def("quantize_rows_into", &quantize_rows_into, "One-group INT4 quantization into views (HIP)");
   m.def("quantize_paged", &quantize_paged, "Grouped INT4 key quantization into packed pages (HIP)");
+  m.def("append_paged", &append_paged,
+        "Decode-time append: one token per sequence, open group re-quantized (HIP)");
   m.def("decode_paged", &decode_paged, "Split-K INT4 flash decoding over paged keys (HIP)");
   m.def("decode_paged_partials", &decode_paged_partials,
         "Decode kernel alone, writing split partials (HIP)");

@@ -157,31 +157,32 @@ int fdi4_quantize_int4(const float* kv, int num_rows, int num_channels, uint8_t*
   return rc != hipSuccess ? rc : f;
 }
 
-int fdi4_quantize_paged(const float* k, int batch, int max_tokens, int64_t k_batch_stride,
-                        int64_t k_head_stride, int64_t k_row_stride, int group_rows,
-                        const fdi4_paged_cache* cache, hipStream_t stream) {
-  int rc = check_cache(cache, false);
+}  // extern "C"
+
+namespace {
+
+// Checks shared by the grouped writers (fdi4_quantize_paged, fdi4_append_paged):
+// group-indexed scales, pages_per_group consistent with group_rows, lengths
+// and page table present, 16-byte stores of packed rows.
+int check_grouped_cache(const fdi4_paged_cache* cache, int group_rows, bool need_values) {
+  int rc = check_cache(cache, need_values);
   if (rc != hipSuccess) return rc;
-  if (!k || !cache->seq_lens || !cache->page_table) return hipErrorInvalidValue;
-  if (batch < 0 || max_tokens < 0 || batch > 65535 || cache->num_kv_heads > 65535)
+  if (!cache->seq_lens || !cache->page_table || cache->num_kv_heads > 65535)
     return hipErrorInvalidValue;
   if (group_rows != 64 && group_rows != 128 && group_rows != 256) return hipErrorInvalidValue;
   if (group_rows % cache->page_rows) return hipErrorInvalidValue;
   if (cache->pages_per_group != group_rows / cache->page_rows || cache->s_page_stride != 0)
     return hipErrorInvalidValue;
-  if ((int64_t)cache->max_pages * cache->page_rows < max_tokens) return hipErrorInvalidValue;
-  // 16-byte row loads of the keys and 16-byte stores of packed rows.
-  if (!aligned(k, 16) || k_batch_stride % 4 || k_head_stride % 4 || k_row_stride % 4 ||
-      k_row_stride < cache->head_dim)
-    return hipErrorInvalidValue;
   if (cache->k_page_stride % 16 || cache->k_head_stride % 16 || cache->k_row_stride % 16 ||
       !aligned(cache->k_pages, 16))
     return hipErrorInvalidValue;
+  return hipSuccess;
+}
+
+QuantPagedArgs quant_args(const fdi4_paged_cache* cache) {
   QuantPagedArgs a;
-  a.k = k;
-  a.k_b = k_batch_stride;
-  a.k_h = k_head_stride;
-  a.k_t = k_row_stride;
+  a.k = nullptr;
+  a.k_b = a.k_h = a.k_t = 0;
   a.seq_lens = cache->seq_lens;
   a.page_table = cache->page_table;
   a.pt_b = cache->pt_batch_stride;
@@ -196,9 +197,72 @@ int fdi4_quantize_paged(const float* k, int batch, int max_tokens, int64_t k_bat
   a.s_g = cache->s_group_stride;
   a.page_rows = cache->page_rows;
   a.num_pages = cache->num_pages;
+  a.max_tokens = 0;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fdi4_quantize_paged(const float* k, int batch, int max_tokens, int64_t k_batch_stride,
+                        int64_t k_head_stride, int64_t k_row_stride, int group_rows,
+                        const fdi4_paged_cache* cache, hipStream_t stream) {
+  int rc = check_grouped_cache(cache, group_rows, false);
+  if (rc != hipSuccess) return rc;
+  if (!k || batch < 0 || max_tokens < 0 || batch > 65535) return hipErrorInvalidValue;
+  if ((int64_t)cache->max_pages * cache->page_rows < max_tokens) return hipErrorInvalidValue;
+  // 16-byte row loads of the keys.
+  if (!aligned(k, 16) || k_batch_stride % 4 || k_head_stride % 4 || k_row_stride % 4 ||
+      k_row_stride < cache->head_dim)
+    return hipErrorInvalidValue;
+  QuantPagedArgs a = quant_args(cache);
+  a.k = k;
+  a.k_b = k_batch_stride;
+  a.k_h = k_head_stride;
+  a.k_t = k_row_stride;
   a.max_tokens = max_tokens;
   return fdi4::launch_quantize_paged(a, cache->head_dim, group_rows, batch, cache->num_kv_heads,
                                      max_tokens, stream);
+}
+
+int fdi4_append_paged(const float* k_new, int64_t kn_batch_stride, int64_t kn_head_stride,
+                      const void* v_new, int64_t vn_batch_stride, int64_t vn_head_stride,
+                      int batch, float* k_stage, int64_t st_batch_stride, int64_t st_head_stride,
+                      int64_t st_row_stride, int group_rows, const fdi4_paged_cache* cache,
+                      hipStream_t stream) {
+  int rc = check_grouped_cache(cache, group_rows, true);
+  if (rc != hipSuccess) return rc;
+  if (!k_new || !v_new || !k_stage || batch < 0 || batch > 65535) return hipErrorInvalidValue;
+  const int D = cache->head_dim;
+  const int veb = cache->v_dtype == FDI4_V_F32 ? 4 : 2;
+  // 16-byte loads and stores of key rows (float4) and value rows.
+  if (!aligned(k_new, 16) || kn_batch_stride % 4 || kn_head_stride % 4 || !aligned(k_stage, 16) ||
+      st_batch_stride % 4 || st_head_stride % 4 || st_row_stride % 4 || st_row_stride < D ||
+      !aligned(v_new, 16) || (vn_batch_stride * veb) % 16 || (vn_head_stride * veb) % 16)
+    return hipErrorInvalidValue;
+  fdi4::AppendArgs a;
+  a.q = quant_args(cache);
+  a.q.k = nullptr;
+  a.q.k_b = a.q.k_h = a.q.k_t = 0;
+  a.q.max_tokens = cache->max_pages * cache->page_rows;
+  a.k_new = k_new;
+  a.kn_b = kn_batch_stride;
+  a.kn_h = kn_head_stride;
+  a.v_new = static_cast<const uint8_t*>(v_new);
+  a.vn_b = vn_batch_stride * veb;
+  a.vn_h = vn_head_stride * veb;
+  a.v_pages = static_cast<uint8_t*>(cache->v_pages);
+  a.vp_page = cache->v_page_stride * veb;
+  a.vp_head = cache->v_head_stride * veb;
+  a.vp_row = cache->v_row_stride * veb;
+  a.v_row_bytes = D * veb;
+  a.stage = k_stage;
+  a.st_b = st_batch_stride;
+  a.st_h = st_head_stride;
+  a.st_r = st_row_stride;
+  a.capacity = cache->max_pages * cache->page_rows;
+  return fdi4::launch_append_paged(a, D, group_rows, batch, cache->num_kv_heads, stream);
 }
 
 int fdi4_decode_num_splits(int batch, int num_q_heads, const fdi4_paged_cache* cache) {
@@ -226,6 +290,8 @@ int fdi4_merge_splits(const float* part_acc, const double* part_ml, int batch, i
   return fdi4::launch_merge(part_acc, part_ml, batch, num_q_heads, head_dim, num_splits, out,
                             out_batch_stride, out_head_stride, stream);
 }
+
+}  // extern "C"
 
 namespace {
 
@@ -295,6 +361,8 @@ int carve_partials(void* workspace, size_t workspace_bytes, int batch, int hq, i
 
 }  // namespace
 
+extern "C" {
+
 int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_batch_stride,
                       int64_t q_head_stride, const fdi4_paged_cache* cache, float* out,
                       int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
@@ -335,6 +403,8 @@ int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
 }
 
 // ---- the reference's dense, shared-stream attention call ----------------------
+
+}  // extern "C"
 
 namespace {
 
@@ -377,6 +447,8 @@ bool dense_args_ok(int B, int H, int D, int nb, int bs) {
 }
 
 }  // namespace
+
+extern "C" {
 
 size_t fdi4_flash_decode_int4_workspace_bytes(int batch_size, int num_heads, int head_dim,
                                               int num_blocks, int block_size) {

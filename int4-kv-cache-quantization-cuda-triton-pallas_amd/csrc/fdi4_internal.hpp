@@ -28,6 +28,22 @@ struct QuantPagedArgs {
   int max_tokens;                       // rows of k; sequence lengths are clamped to it
 };
 
+// Decode-time append of one token per sequence (grouped quantizer re-run over
+// the open group from a staging copy of its key rows).
+struct AppendArgs {
+  QuantPagedArgs q;                     // pages, scales, table, lengths (k unused)
+  const float* k_new;
+  int64_t kn_b, kn_h;                   // elements
+  const uint8_t* v_new;
+  int64_t vn_b, vn_h;                   // bytes
+  uint8_t* v_pages;
+  int64_t vp_page, vp_head, vp_row;     // bytes
+  int v_row_bytes;                      // head_dim * value element size
+  float* stage;
+  int64_t st_b, st_h, st_r;             // elements
+  int capacity;                         // max_pages * page_rows
+};
+
 // Split-K paged decode.
 struct DecodeArgs {
   const float* q;
@@ -61,6 +77,9 @@ size_t rows_workspace_bytes(int64_t rows, int C);
 
 hipError_t launch_quantize_paged(const QuantPagedArgs& a, int D, int group, int batch, int heads,
                                  int max_tokens, hipStream_t st);
+
+hipError_t launch_append_paged(const AppendArgs& a, int D, int group, int batch, int heads,
+                               hipStream_t st);
 
 hipError_t launch_pack(const uint8_t* q, int64_t rows, int C, int64_t q_stride, uint8_t* out,
                        int64_t o_stride, int out_cols, hipStream_t st);

@@ -23,6 +23,12 @@
 //       non-temporal loads held in registers, wave64 min/max reduction,
 //       quantize from registers, nibble pack, and 16-byte non-temporal stores
 //       of whole page rows through the page table.
+//   append_paged_kernel<D, GROUP>
+//       decode-time append: one workgroup per (kv-head, sequence) writes the
+//       token at position seq_lens[b] (value row to its page, key row to the
+//       staging rows of the open group) and re-quantizes that group over its
+//       valid rows, exactly what the grouped quantizer gives for the whole
+//       sequence.
 //   pack_kernel   device form of the nibble packing (reference src/int4_pack.py:14-29)
 
 #include "fdi4_device.hpp"
@@ -176,36 +182,31 @@ hipError_t launch_quantize_rows(const float* kv, int64_t rows, int C, int64_t st
 
 constexpr int kQThreads = 256;
 
-// One workgroup quantizes the rows [g*GROUP, min((g+1)*GROUP, T_b)) of one
-// (sequence b, kv-head h). Thread t owns channels 4*(t % VPR) .. +3 of the
-// rows t / VPR + i * RPI, i < NI; one 16-byte load per owned row.
+// Thread t of a grouped-quantizer workgroup owns channels 4*(t % VPR) .. +3
+// of the group rows t / VPR + i * RPI, i < NI, one 16-byte load per owned row.
 template <int D, int GROUP>
-__global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArgs a) {
-  constexpr int VPR = D / 4;              // threads per row (16 B each)
-  constexpr int RPI = kQThreads / VPR;    // rows covered per sweep
-  constexpr int NI = GROUP / RPI;         // rows per thread
-  constexpr int RB = D / 2;               // packed bytes per row
-  constexpr int NWAVE = kQThreads / 64;
+struct QGeo {
+  static constexpr int VPR = D / 4;              // threads per row (16 B each)
+  static constexpr int RPI = kQThreads / VPR;    // rows covered per sweep
+  static constexpr int NI = GROUP / RPI;         // rows per thread
+  static constexpr int RB = D / 2;               // packed bytes per row
+  static constexpr int NWAVE = kQThreads / 64;
   static_assert(VPR <= 64 && GROUP % RPI == 0, "layout");
+};
 
-  const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int T = min(a.seq_lens[b], a.max_tokens);
-  const int r0 = g * GROUP;
-  if (r0 >= T) return;
-  const int nrows = min(GROUP, T - r0);
+// Quantizes the rows [r0, r0 + nrows) of one (sequence b, kv-head h) whose
+// values the calling threads hold in x (QGeo layout; rows past nrows hold
+// copies of valid rows): per-channel min/max (wave64 butterfly, then LDS
+// across the waves), scale and zero-point of group g, bins from the channel
+// reciprocal (quant_bin_rc), nibble pairs staged in LDS, and whole 16-byte
+// pieces of packed rows stored to their pages through the page table.
+template <int D, int GROUP>
+__device__ __forceinline__ void quantize_group(const QuantPagedArgs& a, int b, int h, int g,
+                                               int r0, int nrows, const float4* x) {
+  using G = QGeo<D, GROUP>;
+  constexpr int VPR = G::VPR, RPI = G::RPI, NI = G::NI, RB = G::RB, NWAVE = G::NWAVE;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int cq = tid % VPR, rsub = tid / VPR;
-
-  const float* src = a.k + (int64_t)b * a.k_b + (int64_t)h * a.k_h + (int64_t)r0 * a.k_t + 4 * cq;
-  // Rows past the valid count load the last valid row again (same lines, no
-  // extra HBM traffic): every register holds a valid value, and duplicates
-  // change neither the minimum nor the maximum.
-  float4 x[NI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int r = min(rsub + i * RPI, nrows - 1);
-    x[i] = ld16f_stream(src + (int64_t)r * a.k_t);
-  }
 
   float mn[4], mx[4];
 #pragma unroll
@@ -289,6 +290,72 @@ __global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArg
   }
 }
 
+// One workgroup quantizes the rows [g*GROUP, min((g+1)*GROUP, T_b)) of one
+// (sequence b, kv-head h) of the key tensor.
+template <int D, int GROUP>
+__global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArgs a) {
+  using G = QGeo<D, GROUP>;
+  const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int T = min(a.seq_lens[b], a.max_tokens);
+  const int r0 = g * GROUP;
+  if (r0 >= T) return;
+  const int nrows = min(GROUP, T - r0);
+  const int cq = threadIdx.x % G::VPR, rsub = threadIdx.x / G::VPR;
+
+  const float* src = a.k + (int64_t)b * a.k_b + (int64_t)h * a.k_h + (int64_t)r0 * a.k_t + 4 * cq;
+  // Rows past the valid count load the last valid row again (same lines, no
+  // extra HBM traffic): every register holds a valid value, and duplicates
+  // change neither the minimum nor the maximum.
+  float4 x[G::NI];
+#pragma unroll
+  for (int i = 0; i < G::NI; ++i) {
+    const int r = min(rsub + i * G::RPI, nrows - 1);
+    x[i] = ld16f_stream(src + (int64_t)r * a.k_t);
+  }
+  quantize_group<D, GROUP>(a, b, h, g, r0, nrows, x);
+}
+
+// Decode-time append: one workgroup per (kv-head, sequence) writes the new
+// token at position t = seq_lens[b] -- its value row into the value page and
+// its key row into the staging rows of the open scale group -- and
+// re-quantizes that group over its t % GROUP + 1 valid rows, which is the
+// grouped quantizer applied to the whole sequence (a partial group is
+// quantized over its valid rows). The new row is taken from k_new, the older
+// rows from the staging buffer, so nothing written here is read back.
+template <int D, int GROUP>
+__global__ __launch_bounds__(kQThreads) void append_paged_kernel(AppendArgs a) {
+  using G = QGeo<D, GROUP>;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int t = a.q.seq_lens[b];
+  if (t < 0 || t >= a.capacity) return;
+  const int g = t / GROUP, rnew = t % GROUP;
+  const int tid = threadIdx.x;
+  const int cq = tid % G::VPR, rsub = tid / G::VPR;
+
+  const float* knew = a.k_new + (int64_t)b * a.kn_b + (int64_t)h * a.kn_h;
+  float* stage = a.stage + (int64_t)b * a.st_b + (int64_t)h * a.st_h;
+  if (tid < G::VPR)
+    *reinterpret_cast<float4*>(stage + (int64_t)rnew * a.st_r + 4 * tid) =
+        *reinterpret_cast<const float4*>(knew + 4 * tid);
+  {
+    const int lp = t / a.q.page_rows, row = t % a.q.page_rows;
+    const int64_t phys =
+        (int64_t)min(max(a.q.page_table[(int64_t)b * a.q.pt_b + lp], 0), a.q.num_pages - 1);
+    const uint8_t* vsrc = a.v_new + (int64_t)b * a.vn_b + (int64_t)h * a.vn_h;
+    uint8_t* vdst = a.v_pages + phys * a.vp_page + (int64_t)h * a.vp_head + (int64_t)row * a.vp_row;
+    for (int o = 16 * tid; o < a.v_row_bytes; o += 16 * kQThreads) st16(vdst + o, ld16(vsrc + o));
+  }
+
+  float4 x[G::NI];
+#pragma unroll
+  for (int i = 0; i < G::NI; ++i) {
+    const int r = min(rsub + i * G::RPI, rnew);
+    const float* src = (r == rnew) ? knew : stage + (int64_t)r * a.st_r;
+    x[i] = *reinterpret_cast<const float4*>(src + 4 * cq);
+  }
+  quantize_group<D, GROUP>(a.q, b, h, g, g * GROUP, rnew + 1, x);
+}
+
 hipError_t launch_quantize_paged(const QuantPagedArgs& a, int D, int group, int batch, int heads,
                                  int max_tokens, hipStream_t st) {
   const int ngroups = (max_tokens + group - 1) / group;
@@ -303,6 +370,22 @@ hipError_t launch_quantize_paged(const QuantPagedArgs& a, int D, int group, int 
   FDI4_QP(128, 64) FDI4_QP(128, 128) FDI4_QP(128, 256)
   FDI4_QP(256, 64) FDI4_QP(256, 128) FDI4_QP(256, 256)
 #undef FDI4_QP
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_append_paged(const AppendArgs& a, int D, int group, int batch, int heads,
+                               hipStream_t st) {
+  if (batch == 0 || heads == 0) return hipSuccess;
+  dim3 grid(heads, batch);
+#define FDI4_AP(DD, GG)                                                                  \
+  if (D == DD && group == GG) {                                                          \
+    hipLaunchKernelGGL((append_paged_kernel<DD, GG>), grid, dim3(kQThreads), 0, st, a);   \
+    return hipGetLastError();                                                            \
+  }
+  FDI4_AP(64, 64) FDI4_AP(64, 128) FDI4_AP(64, 256)
+  FDI4_AP(128, 64) FDI4_AP(128, 128) FDI4_AP(128, 256)
+  FDI4_AP(256, 64) FDI4_AP(256, 128) FDI4_AP(256, 256)
+#undef FDI4_AP
   return hipErrorInvalidValue;
 }
 

@@ -54,6 +54,9 @@ SIGNATURES = {
                                    c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "fdi4_quantize_paged": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64, c_int64, c_int,
                                     ctypes.POINTER(PagedCache), c_void_p]),
+    "fdi4_append_paged": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int,
+                                  c_void_p, c_int64, c_int64, c_int64, c_int,
+                                  ctypes.POINTER(PagedCache), c_void_p]),
     "fdi4_flash_decode_int4": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
                                        c_void_p]),

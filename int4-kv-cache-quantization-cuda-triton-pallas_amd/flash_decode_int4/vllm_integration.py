@@ -149,3 +149,170 @@ class INT4PagedKVCache:
             "fp16_equiv_mb": round(fp16_equiv / 1048576, 3),
             "ratio": round(fp16_equiv / max(stored, 1), 2),
         }
+
+
+class INT4PagedSequenceCache:
+    """Batched per-sequence INT4 cache in the decode kernel's native layout.
+
+    The batched counterpart of the reference's page-table cache
+    (src/vllm_integration.py:29-102): sequences, kv-heads and 128-token scale
+    groups instead of one shared block stream, and a decode-time append that
+    writes one token per sequence per step on the device.
+
+      k_pages    uint8 [num_pages, kv_heads, page_rows, D/2]  nibble-packed keys
+      v_pages    float32 or float16 [num_pages, kv_heads, page_rows, D]
+      k_scale    float32 [max_seqs, kv_heads, max_groups, D]  (and k_zp)
+      page_table int32 [max_seqs, max_pages_per_seq]
+      seq_lens   int32 [max_seqs]
+      k_stage    float32 [max_seqs, kv_heads, group_rows, D]  float keys of
+                 each sequence's open (partial) scale group
+
+    Sequences 0..B-1 of a call are the first B slots. Pages come from a host
+    free list; the page table is updated on the device when a sequence enters
+    a new page. A partial last group is quantized over its valid rows, so after
+    any mix of prefill and append the pages and scales equal the grouped
+    quantizer applied to each whole sequence (reference
+    tests/test_perplexity_harness.py:122-131).
+    """
+
+    def __init__(self, num_pages: int, num_kv_heads: int, head_dim: int, max_seqs: int,
+                 max_seq_len: int, page_rows: int = 16, group_rows: int = 128,
+                 value_dtype: str = "float32"):
+        import torch
+        ops._require_device(None)
+        if head_dim not in (64, 128, 256):
+            raise ValueError(f"head_dim must be 64, 128 or 256, got {head_dim}")
+        if group_rows not in (64, 128, 256) or group_rows % page_rows:
+            raise ValueError("group_rows must be 64, 128 or 256 and a multiple of page_rows")
+        if value_dtype not in ("float32", "float16"):
+            raise ValueError("value_dtype must be float32 or float16")
+        if min(num_pages, num_kv_heads, max_seqs, max_seq_len, page_rows) < 1:
+            raise ValueError("sizes must be positive")
+        self.num_pages, self.num_kv_heads, self.head_dim = num_pages, num_kv_heads, head_dim
+        self.max_seqs, self.page_rows, self.group_rows = max_seqs, page_rows, group_rows
+        self.max_pages_per_seq = (max_seq_len + page_rows - 1) // page_rows
+        groups = (self.max_pages_per_seq * page_rows + group_rows - 1) // group_rows
+        dev = torch.device("cuda")
+        vdt = torch.float16 if value_dtype == "float16" else torch.float32
+        H, D = num_kv_heads, head_dim
+        self.k_pages = torch.zeros(num_pages, H, page_rows, D // 2, dtype=torch.uint8, device=dev)
+        self.v_pages = torch.zeros(num_pages, H, page_rows, D, dtype=vdt, device=dev)
+        self.k_scale = torch.zeros(max_seqs, H, groups, D, dtype=torch.float32, device=dev)
+        self.k_zp = torch.zeros_like(self.k_scale)
+        self.page_table = torch.zeros(max_seqs, self.max_pages_per_seq, dtype=torch.int32,
+                                      device=dev)
+        self.seq_lens = torch.zeros(max_seqs, dtype=torch.int32, device=dev)
+        self.k_stage = torch.zeros(max_seqs, H, group_rows, D, dtype=torch.float32, device=dev)
+        self._free = list(range(num_pages - 1, -1, -1))
+        self._pages = [[] for _ in range(max_seqs)]
+        self._lens = np.zeros(max_seqs, dtype=np.int64)
+
+    # ---- page bookkeeping (host) -------------------------------------------
+
+    def _grow(self, b: int, n_tokens: int, updates: list) -> None:
+        need = (n_tokens + self.page_rows - 1) // self.page_rows
+        if need > self.max_pages_per_seq:
+            raise ValueError(f"sequence {b} would hold {n_tokens} tokens; the cache holds "
+                             f"{self.max_pages_per_seq * self.page_rows} per sequence")
+        while len(self._pages[b]) < need:
+            if not self._free:
+                raise RuntimeError("out of pages")
+            p = self._free.pop()
+            updates.append((b, len(self._pages[b]), p))
+            self._pages[b].append(p)
+
+    def _apply(self, updates: list) -> None:
+        import torch
+        if not updates:
+            return
+        u = torch.tensor(updates, dtype=torch.int64).cuda()
+        self.page_table[u[:, 0], u[:, 1]] = u[:, 2].to(torch.int32)
+
+    def free(self, b: int) -> None:
+        """Release sequence b's pages; its slot starts empty."""
+        self._free.extend(reversed(self._pages[b]))
+        self._pages[b] = []
+        self._lens[b] = 0
+        self.seq_lens[b] = 0
+
+    # ---- writes ------------------------------------------------------------
+
+    def prefill(self, k, v, seq_lens) -> None:
+        """Start sequences 0..B-1 from k, v [B, kv_heads, T, D] (keys float32,
+        values in the cache's dtype) with seq_lens[b] <= T valid tokens."""
+        import torch
+        lens = np.asarray(seq_lens.cpu() if hasattr(seq_lens, "cpu") else seq_lens, np.int64)
+        B, H, T, D = k.shape
+        if (H, D) != (self.num_kv_heads, self.head_dim) or tuple(v.shape) != tuple(k.shape):
+            raise ValueError("k and v must be [batch, kv_heads, tokens, head_dim] of this cache")
+        if B > self.max_seqs or len(lens) != B or (lens < 0).any() or (lens > T).any():
+            raise ValueError("bad batch size or sequence lengths")
+        updates = []
+        for b in range(B):
+            self.free(b)
+            self._grow(b, int(lens[b]), updates)
+        self._apply(updates)
+        lens_t = torch.as_tensor(lens, dtype=torch.int32).cuda()
+        self.seq_lens[:B] = lens_t
+        self._lens[:B] = lens
+        ops.quantize_int4_paged(k, self.seq_lens[:B], self.page_table[:B], self.k_pages,
+                                self.k_scale[:B], self.k_zp[:B], self.group_rows)
+        # Values: token t of sequence b -> page_table[b, t // page_rows], row t % page_rows.
+        bi, ti = np.nonzero(np.arange(T)[None, :] < lens[:, None])
+        if len(bi):
+            pages = torch.as_tensor(np.array([self._pages[b][t // self.page_rows]
+                                              for b, t in zip(bi, ti)]), device="cuda")
+            rows = torch.as_tensor(ti % self.page_rows, device="cuda")
+            bt, tt = torch.as_tensor(bi, device="cuda"), torch.as_tensor(ti, device="cuda")
+            self.v_pages[pages, :, rows, :] = v[bt, :, tt, :].to(self.v_pages.dtype)
+        # Open groups: the float keys of each sequence's partial last group.
+        for b in range(B):
+            r = int(lens[b]) % self.group_rows
+            if r:
+                g0 = int(lens[b]) - r
+                self.k_stage[b, :, :r] = k[b, :, g0:g0 + r]
+
+    def append(self, k_new, v_new) -> None:
+        """Append one token to each of sequences 0..B-1: k_new float32 and v_new
+        (the cache's value dtype) [B, kv_heads, D]. One kernel launch."""
+        B = k_new.shape[0]
+        if B > self.max_seqs or tuple(k_new.shape) != (B, self.num_kv_heads, self.head_dim):
+            raise ValueError("k_new must be [batch <= max_seqs, kv_heads, head_dim]")
+        updates = []
+        for b in range(B):
+            self._grow(b, int(self._lens[b]) + 1, updates)
+        self._apply(updates)
+        load_binding().append_paged(k_new, v_new.to(self.v_pages.dtype), self.k_stage[:B],
+                                    self.k_pages, self.v_pages, self.k_scale[:B],
+                                    self.k_zp[:B], self.page_table[:B], self.seq_lens[:B],
+                                    self.group_rows)
+        self.seq_lens[:B] += 1
+        self._lens[:B] += 1
+
+    # ---- reads -------------------------------------------------------------
+
+    def decode(self, query, num_splits: int = 0):
+        """Fused INT4 attention of query [B, Hq, D] (float32, Hq a multiple of
+        kv_heads) over sequences 0..B-1; returns float32 [B, Hq, D]."""
+        B = query.shape[0]
+        return ops.flash_decode_paged(query, self.k_pages, self.v_pages, self.k_scale[:B],
+                                      self.k_zp[:B], self.page_table[:B], self.seq_lens[:B],
+                                      self.group_rows, num_splits,
+                                      max_pages=self.max_pages_per_seq)
+
+    def lengths(self) -> np.ndarray:
+        return self._lens.copy()
+
+    def memory_stats(self) -> dict:
+        """Bytes of the pages in use (packed keys, values, their scale groups)
+        against the same tokens as fp16 K + V."""
+        used = sum(len(p) for p in self._pages)
+        H, D, pr = self.num_kv_heads, self.head_dim, self.page_rows
+        vb = self.v_pages.element_size()
+        stored = used * H * pr * (D // 2 + D * vb) + int(
+            sum((n + self.group_rows - 1) // self.group_rows for n in self._lens)) * H * D * 8
+        tokens = int(self._lens.sum())
+        fp16 = tokens * H * D * 2 * 2
+        return {"pages": used, "tokens": tokens, "stored_mb": round(stored / 1048576, 3),
+                "fp16_equiv_mb": round(fp16 / 1048576, 3),
+                "ratio": round(fp16 / max(stored, 1), 2)}

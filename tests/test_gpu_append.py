@@ -1,0 +1,131 @@
+"""Decode-time append (one token per sequence per step) into the batched INT4
+cache: after any mix of prefill and appends the packed pages, group scales
+and values must equal the grouped quantizer applied to each whole sequence
+(a partial group is quantized over its valid rows, reference
+tests/test_perplexity_harness.py:122-131), bit for bit, and the decode over
+the result must match the page-loop oracle."""
+
+import numpy as np
+import pytest
+
+from oracle import pack_int4, paged_decode_f64, paged_decode_ref, quantize_groups_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _cache(**kw):
+    from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
+    return INT4PagedSequenceCache(**kw)
+
+
+def _check_against_oracle(cache, streams, lens, group, vdtype):
+    """streams[b] = (K [H, n, D] float32, V [H, n, D]) of sequence b's tokens."""
+    B = len(streams)
+    H, _, D = streams[0][0].shape
+    T = max(max(lens), 1)
+    k = np.zeros((B, H, T, D), np.float32)
+    for b, (kb, _) in enumerate(streams):
+        k[b, :, :lens[b]] = kb[:, :lens[b]]
+    qr, sr, zr = quantize_groups_ref(k, np.array(lens), group_size=group)
+    kp = cache.k_pages.cpu().numpy()
+    vp = cache.v_pages.float().cpu().numpy()
+    sc = cache.k_scale.cpu().numpy()
+    zc = cache.k_zp.cpu().numpy()
+    table = cache.page_table.cpu().numpy()
+    assert list(cache.seq_lens[:B].cpu().numpy()) == list(lens)
+    for b in range(B):
+        ng = (lens[b] + group - 1) // group
+        np.testing.assert_array_equal(sc[b, :, :ng], sr[b, :, :ng])
+        np.testing.assert_array_equal(zc[b, :, :ng], zr[b, :, :ng])
+        vb = streams[b][1]
+        for lp in range((lens[b] + 15) // 16):
+            n = min(16, lens[b] - lp * 16)
+            np.testing.assert_array_equal(kp[table[b, lp], :, :n],
+                                          pack_int4(qr[b, :, lp * 16:lp * 16 + n]))
+            np.testing.assert_array_equal(vp[table[b, lp], :, :n],
+                                          vb[:, lp * 16:lp * 16 + n].astype(vdtype)
+                                          .astype(np.float32))
+    return table
+
+
+@pytest.mark.parametrize("D,group,vdtype,H", [(128, 128, "float32", 2), (64, 64, "float16", 3),
+                                              (256, 256, "float32", 1)])
+def test_append_equals_whole_sequence_quantization(D, group, vdtype, H):
+    import torch
+    rng = np.random.RandomState(D + group)
+    B, steps = 3, 150
+    lens0 = [0, group - 1, 2 * group - 56]  # empty, one short of a group, mid-group
+    total = [n + steps for n in lens0]
+    streams = [(rng.randn(H, n, D).astype(np.float32), rng.randn(H, n, D).astype(np.float32))
+               for n in total]
+    cache = _cache(num_pages=128, num_kv_heads=H, head_dim=D, max_seqs=4,
+                   max_seq_len=max(total) + 16, group_rows=group, value_dtype=vdtype)
+    T0 = max(lens0)
+    k0 = np.zeros((B, H, T0, D), np.float32)
+    v0 = np.zeros((B, H, T0, D), np.float32)
+    for b in range(B):
+        k0[b, :, :lens0[b]] = streams[b][0][:, :lens0[b]]
+        v0[b, :, :lens0[b]] = streams[b][1][:, :lens0[b]]
+    vt = torch.float16 if vdtype == "float16" else torch.float32
+    cache.prefill(torch.from_numpy(k0).cuda(), torch.from_numpy(v0).cuda().to(vt), lens0)
+    for s in range(steps):
+        kn = np.stack([streams[b][0][:, lens0[b] + s] for b in range(B)])
+        vn = np.stack([streams[b][1][:, lens0[b] + s] for b in range(B)])
+        cache.append(torch.from_numpy(kn).cuda(), torch.from_numpy(vn).cuda().to(vt))
+        if s in (0, 1, 57):  # partial states are exact too
+            _check_against_oracle(cache, streams, [n + s + 1 for n in lens0], group, vdtype)
+    table = _check_against_oracle(cache, streams, total, group, vdtype)
+
+    # The decode over the appended cache matches the page-loop oracle (q-heads
+    # grouped two per kv-head).
+    q = rng.randn(B, 2 * H, D).astype(np.float32)
+    got = cache.decode(torch.from_numpy(q).cuda()).cpu().numpy()
+    args = (q, cache.k_pages.cpu().numpy(), cache.v_pages.float().cpu().numpy(),
+            cache.k_scale[:B].cpu().numpy(), cache.k_zp[:B].cpu().numpy(), table[:B],
+            np.array(total), 16, group)
+    o32, o64 = paged_decode_ref(*args), paged_decode_f64(*args)
+    assert np.abs(got - o32).max() <= max(TOL, 1.25 * np.abs(o32 - o64).max())
+
+
+def test_append_matches_prefill_of_the_same_tokens():
+    """Prefill of T tokens and prefill of T-40 plus 40 appends store the same
+    bytes (pages may differ; compare through the page tables)."""
+    import torch
+    rng = np.random.RandomState(3)
+    B, H, D, T = 2, 4, 128, 300
+    k = rng.randn(B, H, T, D).astype(np.float32)
+    v = rng.randn(B, H, T, D).astype(np.float32)
+    a = _cache(num_pages=64, num_kv_heads=H, head_dim=D, max_seqs=B, max_seq_len=T)
+    b_ = _cache(num_pages=64, num_kv_heads=H, head_dim=D, max_seqs=B, max_seq_len=T)
+    a.prefill(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), [T, T])
+    b_.prefill(torch.from_numpy(k[:, :, :T - 40]).cuda(), torch.from_numpy(v[:, :, :T - 40]).cuda(),
+               [T - 40, T - 40])
+    for t in range(T - 40, T):
+        b_.append(torch.from_numpy(np.ascontiguousarray(k[:, :, t])).cuda(),
+                  torch.from_numpy(np.ascontiguousarray(v[:, :, t])).cuda())
+    for c in (a, b_):
+        c.kp, c.vp, c.tb = (c.k_pages.cpu().numpy(), c.v_pages.cpu().numpy(),
+                            c.page_table.cpu().numpy())
+    for bi in range(B):
+        for lp in range((T + 15) // 16):
+            n = min(16, T - lp * 16)
+            np.testing.assert_array_equal(a.kp[a.tb[bi, lp], :, :n], b_.kp[b_.tb[bi, lp], :, :n])
+            np.testing.assert_array_equal(a.vp[a.tb[bi, lp], :, :n], b_.vp[b_.tb[bi, lp], :, :n])
+    np.testing.assert_array_equal(a.k_scale.cpu().numpy(), b_.k_scale.cpu().numpy())
+    q = torch.from_numpy(rng.randn(B, H, D).astype(np.float32)).cuda()
+    assert torch.equal(a.decode(q), b_.decode(q))
+
+
+def test_capacity_and_shapes_are_checked():
+    import torch
+    c = _cache(num_pages=4, num_kv_heads=1, head_dim=64, max_seqs=1, max_seq_len=32)
+    k = torch.zeros(1, 1, 32, 64, device="cuda")
+    c.prefill(k, k.clone(), [32])
+    with pytest.raises(ValueError, match="holds"):
+        c.append(torch.zeros(1, 1, 64, device="cuda"), torch.zeros(1, 1, 64, device="cuda"))
+    with pytest.raises(ValueError):
+        c.append(torch.zeros(1, 2, 64, device="cuda"), torch.zeros(1, 2, 64, device="cuda"))
+    c.free(0)
+    assert c.lengths()[0] == 0 and c.memory_stats()["pages"] == 0

@@ -202,6 +202,20 @@ class TestCABI:
             assert hasattr(lib, name), name
         assert set(declared) == set(capi.SIGNATURES), "ctypes table and header disagree"
 
+    def test_only_declared_symbols_are_exported(self):
+        """Internal helpers stay out of the library's dynamic symbol table."""
+        import shutil
+        import subprocess
+        from flash_decode_int4 import capi
+        nm = shutil.which("nm")
+        if nm is None:
+            pytest.skip("nm not available")
+        out = subprocess.run([nm, "-D", "--defined-only", capi.LIB_PATH],
+                             capture_output=True, text=True, check=True).stdout
+        names = {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+        public = {n for n in names if not n.startswith("_")}
+        assert public == set(self._declared())
+
     def test_size_queries(self):
         from flash_decode_int4 import capi
         lib = capi.load()
