@@ -79,7 +79,7 @@ def build_sets(name, value_dtype, n_sets_hint=0, seq_lens=None):
                                     backend="torch", seed=1234)
     vbytes = 2 if value_dtype == "float16" else 4
     set_bytes = workloads.decode_bytes(first["seq_lens"], first["heads"], first["head_dim"],
-                                       vbytes)
+                                       vbytes, q_heads=first["q_heads"])
     if n_sets_hint:
         n_sets = n_sets_hint
     else:
@@ -113,12 +113,12 @@ def time_decode(sets, splits, steps, warmup):
     from flash_decode_int4._lib import load_binding
     C = load_binding()
     w0 = sets[0]["w"]
-    B, H, D = w0["batch"], w0["heads"], w0["head_dim"]
+    B, H, D, Hq = w0["batch"], w0["heads"], w0["head_dim"], w0["q_heads"]
     ppg = w0["group_rows"] // w0["page_rows"]
     maxp = w0["page_table"].shape[1]
-    S = splits or int(C.decode_num_splits(B, H, maxp, w0["page_rows"]))
+    S = splits or int(C.decode_num_splits(B, Hq, H, D, maxp, w0["page_rows"]))
     S = max(1, min(S, maxp * ((w0["page_rows"] + 15) // 16)))
-    parts = torch.empty(int(C.decode_partials_bytes(B, H, D, S)), dtype=torch.uint8,
+    parts = torch.empty(int(C.decode_partials_bytes(B, Hq, D, S)), dtype=torch.uint8,
                         device="cuda")
 
     def step(i):
@@ -132,7 +132,7 @@ def time_decode(sets, splits, steps, warmup):
                                   st["sl"], None, ppg, maxp, 1)
         C.decode_paged_partials(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
                                 st["sl"], None, ppg, maxp, S, parts)
-        return C.merge_splits(parts, B, H, D, S)
+        return C.merge_splits(parts, B, Hq, D, S)
 
     def decode_only(i):
         st = sets[i % len(sets)]
@@ -285,7 +285,8 @@ def cpu_baseline(st, gpu_out, runs, vbytes):
                 break
         if not pages_ok:
             break
-    nbytes = workloads.decode_bytes(host["sl"], w["heads"], w["head_dim"], vbytes)
+    nbytes = workloads.decode_bytes(host["sl"], w["heads"], w["head_dim"], vbytes,
+                                    q_heads=w["q_heads"])
     qbytes = workloads.quantize_bytes(host["sl"], w["heads"], w["head_dim"])
     t = median(times)
     base = {
@@ -438,10 +439,14 @@ def main():
         "data": "synthetic N(0,1) q/K/V, seeded; keys quantized on the GPU; random page "
                 "permutation",
         "config": {
-            "workload": (f"{args.workload}: B{w0['batch']} H{w0['heads']} D{w0['head_dim']} "
+            "workload": (f"{args.workload}: B{w0['batch']} "
+                         + (f"H{w0['heads']} " if w0["q_heads"] == w0["heads"]
+                            else f"Hkv{w0['heads']} Hq{w0['q_heads']} ")
+                         + f"D{w0['head_dim']} "
                          f"T{int(max(w0['seq_lens']))}, {w0['page_rows']}-token pages, "
                          f"{w0['group_rows']}-token scale groups, {args.value_dtype} values"),
-            "batch": w0["batch"], "heads": w0["heads"], "head_dim": w0["head_dim"],
+            "batch": w0["batch"], "heads": w0["heads"], "q_heads": w0["q_heads"],
+            "head_dim": w0["head_dim"],
             "max_tokens": int(max(w0["seq_lens"])), "page_rows": w0["page_rows"],
             "group_rows": w0["group_rows"], "num_splits": res["splits"],
             "input_sets": len(sets), "bytes_per_step": set_bytes,
@@ -468,7 +473,10 @@ def main():
             "unit": "GB/s",
             "frac": round(set_bytes / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": f"decode_kernel<D={w0['head_dim']}, {args.value_dtype} values>",
+            "kernel": (f"decode_kernel<D={w0['head_dim']}, {args.value_dtype} values>"
+                       if w0["q_heads"] == w0["heads"] else
+                       f"decode_gqa_kernel<D={w0['head_dim']}, {args.value_dtype} values, "
+                       f"{w0['q_heads'] // w0['heads']} q-heads per kv-head>"),
         },
     }
     if not args.no_pmc:

@@ -158,14 +158,17 @@ int fdi4_flash_decode_int4_ws(const float* query, const uint8_t* k_q, const floa
                               int block_size, float* output, void* workspace,
                               size_t workspace_bytes, hipStream_t stream);
 
-/* Split count the decode would choose for this shape when num_splits <= 0. */
+/* Split count the decode would choose for this shape when num_splits <= 0
+ * (reads cache->num_kv_heads, head_dim, max_pages and page_rows only; 1 when
+ * num_kv_heads does not divide num_q_heads). */
 int fdi4_decode_num_splits(int batch, int num_q_heads, const fdi4_paged_cache* cache);
 
 /* Workspace for fdi4_decode_paged with the given split count (0 when 1). */
 size_t fdi4_decode_workspace_bytes(int batch, int num_q_heads, int head_dim, int num_splits);
 
 /* Split-K paged decode: out[b, h, :] = softmax(q[b,h].K^T) V over the valid
- * rows of sequence b, kv-head h / (num_q_heads / num_kv_heads); unscaled
+ * rows of sequence b, kv-head h / (num_q_heads / num_kv_heads) (up to eight
+ * q-heads of one kv-head share a workgroup and one read of its pages); unscaled
  * logits; empty pages skipped; a sequence with no valid row gives exact
  * zeros. num_splits <= 0 selects fdi4_decode_num_splits. With more than one
  * split the partials go to the workspace and the merge kernel runs on the

@@ -399,8 +399,11 @@ int64_t decode_partials_bytes(int64_t batch, int64_t q_heads, int64_t head_dim,
                                              (int)num_splits);
 }
 
-int64_t decode_num_splits(int64_t batch, int64_t q_heads, int64_t max_pages, int64_t page_rows) {
+int64_t decode_num_splits(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                          int64_t max_pages, int64_t page_rows) {
   fdi4_paged_cache c = {};
+  c.num_kv_heads = (int32_t)kv_heads;
+  c.head_dim = (int32_t)head_dim;
   c.max_pages = (int32_t)max_pages;
   c.page_rows = (int32_t)page_rows;
   return fdi4_decode_num_splits((int)batch, (int)q_heads, &c);

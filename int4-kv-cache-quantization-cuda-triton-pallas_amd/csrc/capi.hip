@@ -57,14 +57,41 @@ int pick_waves(int chunks) {
   return chunks >= 8 * kMinChunksPerWave ? 8 : 4;
 }
 
-int auto_splits(int batch, int hq, int chunks) {
-  if (chunks <= 0) return 1;
-  const int waves = pick_waves(chunks);
+// Query heads one decode workgroup serves (heads of one kv-head, so their
+// keys and values are read once for all of them): the largest of 8, 4, 2 that
+// divides Hq/Hkv within what registers and LDS allow (8 at D=64, 4 at D=128
+// and 256); 1 runs the per-head kernel. FDI4_DECODE_HEADS_PER_WG caps the
+// choice (tuning; 1 disables grouping).
+int pick_heads_per_wg(int d, int hq_per_kv) {
+  const int cap = std::min(env_int("FDI4_DECODE_HEADS_PER_WG", 8), d == 64 ? 8 : 4);
+  for (int hg : {8, 4, 2})
+    if (hg <= cap && hq_per_kv % hg == 0) return hg;
+  return 1;
+}
+
+struct DecodePlan {
+  int heads_per_wg;
+  int waves;
+  int splits;
+};
+
+// Launch shape of a decode: heads per workgroup, waves per workgroup (the
+// grouped kernel at D=256 has registers for four), and the split count that
+// gives about kTargetWaves waves over the (sequence, head group) streams.
+DecodePlan plan_decode(int batch, int hq, int hq_per_kv, int d, int chunks) {
+  DecodePlan p;
+  p.heads_per_wg = pick_heads_per_wg(d, hq_per_kv);
+  p.waves = (p.heads_per_wg > 1 && d == 256) ? 4 : pick_waves(chunks);
+  if (chunks <= 0) {
+    p.splits = 1;
+    return p;
+  }
   const int64_t target = env_int("FDI4_DECODE_TARGET_WAVES", kTargetWaves);
-  const int64_t per_split = (int64_t)batch * hq * waves;
-  int s = (int)((target + per_split - 1) / per_split);
-  const int smax = std::max(1, chunks / (waves * kMinChunksPerWave));
-  return std::max(1, std::min(s, smax));
+  const int64_t per_split = (int64_t)batch * (hq / p.heads_per_wg) * p.waves;
+  const int s = (int)((target + per_split - 1) / per_split);
+  const int smax = std::max(1, chunks / (p.waves * kMinChunksPerWave));
+  p.splits = std::max(1, std::min(s, smax));
+  return p;
 }
 
 size_t decode_ws_bytes(int batch, int hq, int d, int splits) {
@@ -266,8 +293,12 @@ int fdi4_append_paged(const float* k_new, int64_t kn_batch_stride, int64_t kn_he
 }
 
 int fdi4_decode_num_splits(int batch, int num_q_heads, const fdi4_paged_cache* cache) {
-  if (!cache || batch <= 0 || num_q_heads <= 0 || cache->page_rows < 1) return 1;
-  return auto_splits(batch, num_q_heads, chunks_per_seq(cache));
+  if (!cache || batch <= 0 || num_q_heads <= 0 || cache->page_rows < 1 ||
+      cache->num_kv_heads < 1 || num_q_heads % cache->num_kv_heads)
+    return 1;
+  return plan_decode(batch, num_q_heads, num_q_heads / cache->num_kv_heads, cache->head_dim,
+                     chunks_per_seq(cache))
+      .splits;
 }
 
 size_t fdi4_decode_workspace_bytes(int batch, int num_q_heads, int head_dim, int num_splits) {
@@ -296,6 +327,13 @@ int fdi4_merge_splits(const float* part_acc, const double* part_ml, int batch, i
 namespace {
 
 // Validate and fill the kernel argument block shared by the decode entry points.
+hipError_t launch_decode_any(const DecodeArgs& a, int d, int v_dtype, int batch,
+                             hipStream_t stream) {
+  if (a.heads_per_wg > 1)
+    return fdi4::launch_decode_gqa(a, d, v_dtype, batch, a.heads_per_wg, stream);
+  return fdi4::launch_decode(a, d, v_dtype, batch, stream);
+}
+
 int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_batch_stride,
                      int64_t q_head_stride, const fdi4_paged_cache* cache, int num_splits,
                      DecodeArgs* a) {
@@ -306,7 +344,9 @@ int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_b
   if (num_q_heads % cache->num_kv_heads) return hipErrorInvalidValue;
   if (cache->page_table && cache->pt_batch_stride < 0) return hipErrorInvalidValue;
   const int chunks = chunks_per_seq(cache);
-  int splits = num_splits > 0 ? num_splits : auto_splits(batch, num_q_heads, chunks);
+  const DecodePlan plan = plan_decode(batch, num_q_heads, num_q_heads / cache->num_kv_heads,
+                                      cache->head_dim, chunks);
+  int splits = num_splits > 0 ? num_splits : plan.splits;
   splits = std::max(1, std::min(splits, std::max(chunks, 1)));
   a->q = query;
   a->q_b = q_batch_stride;
@@ -343,7 +383,8 @@ int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_b
   a->ws_acc = nullptr;
   a->ws_ml = nullptr;
   a->final_out = 0;
-  a->waves = pick_waves(chunks);
+  a->waves = plan.waves;
+  a->heads_per_wg = plan.heads_per_wg;
   return hipSuccess;
 }
 
@@ -378,11 +419,11 @@ int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_
   a.o_h = out_head_stride;
   if (a.num_splits == 1) {
     a.final_out = 1;
-    return fdi4::launch_decode(a, d, cache->v_dtype, batch, stream);
+    return launch_decode_any(a, d, cache->v_dtype, batch, stream);
   }
   rc = carve_partials(workspace, workspace_bytes, batch, num_q_heads, d, &a);
   if (rc != hipSuccess) return rc;
-  hipError_t e = fdi4::launch_decode(a, d, cache->v_dtype, batch, stream);
+  hipError_t e = launch_decode_any(a, d, cache->v_dtype, batch, stream);
   if (e != hipSuccess) return e;
   return fdi4::launch_merge(a.ws_acc, a.ws_ml, batch, num_q_heads, d, a.num_splits, out,
                             out_batch_stride, out_head_stride, stream);
@@ -399,7 +440,7 @@ int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
   if (a.num_splits != num_splits) return hipErrorInvalidValue;  // the layout must be exact
   rc = carve_partials(partials, partials_bytes, batch, num_q_heads, cache->head_dim, &a);
   if (rc != hipSuccess) return rc;
-  return fdi4::launch_decode(a, cache->head_dim, cache->v_dtype, batch, stream);
+  return launch_decode_any(a, cache->head_dim, cache->v_dtype, batch, stream);
 }
 
 // ---- the reference's dense, shared-stream attention call ----------------------
@@ -434,7 +475,8 @@ DenseLayout dense_layout(int B, int H, int D, int nb, int bs) {
     L.off_o = off;
     off += align_up((size_t)B * H * L.dp * sizeof(float));
   }
-  L.splits = auto_splits(B, H, nb * ceil_div(bs, 16));
+  // Every (sequence, head) attends the one shared page stream (kv-heads = 1).
+  L.splits = plan_decode(B, H, H, L.dp, nb * ceil_div(bs, 16)).splits;
   L.off_part = off;
   off += decode_ws_bytes(B, H, L.dp, L.splits);
   L.total = std::max<size_t>(off, kAlign);

@@ -64,6 +64,7 @@ struct DecodeArgs {
   int chunks_per_split, num_splits, num_q_heads;
   int final_out;                        // 1: normalized output; 0: split partials
   int waves;                            // wave64s per workgroup (4 or 8)
+  int heads_per_wg;                     // q-heads per workgroup (1: per-head kernel)
   float* out;
   int64_t o_b, o_h;
   float* ws_acc;                        // [B, Hq, S, D]
@@ -85,6 +86,9 @@ hipError_t launch_pack(const uint8_t* q, int64_t rows, int C, int64_t q_stride, 
                        int64_t o_stride, int out_cols, hipStream_t st);
 
 hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hipStream_t st);
+
+hipError_t launch_decode_gqa(const DecodeArgs& a, int D, int v_dtype, int batch, int hg,
+                             hipStream_t st);
 
 hipError_t launch_merge(const float* ws_acc, const double* ws_ml, int batch, int hq, int D,
                         int splits, float* out, int64_t o_b, int64_t o_h, hipStream_t st);

@@ -25,7 +25,7 @@ CSRC = os.path.join(ROOT_DIR, "csrc")
 INCLUDE = os.path.join(os.path.dirname(ROOT_DIR), "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_SOURCES = ("quantize.hip", "decode.hip", "capi.hip")
+HIP_SOURCES = ("quantize.hip", "decode.hip", "decode_gqa.hip", "capi.hip")
 LIB_PATH = os.path.join(PKG_DIR, "libfdi4.so")
 EXT_PATH = os.path.join(PKG_DIR, "_C.so")
 
@@ -56,11 +56,25 @@ def _run(cmd, verbose):
 
 
 def build_library(verbose=False):
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
-    tmp = LIB_PATH + ".tmp"
-    cmd = [os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, "-shared", "-I", INCLUDE,
-           *srcs, "-o", tmp]
-    _run(cmd, verbose)
+    """One hipcc per source in parallel (each object carries its own gfx950
+    code object), then one link."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    with tempfile.TemporaryDirectory(prefix="fdi4_build_") as tmpdir:
+        objs = []
+        cmds = []
+        for src in HIP_SOURCES:
+            obj = os.path.join(tmpdir, src + ".o")
+            objs.append(obj)
+            cmds.append([hipcc, *HIPCC_FLAGS, "-I", INCLUDE, "-c", os.path.join(CSRC, src),
+                         "-o", obj])
+        workers = max(1, min(len(cmds), os.cpu_count() or 1))
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            for fut in [pool.submit(_run, c, verbose) for c in cmds]:
+                fut.result()
+        tmp = LIB_PATH + ".tmp"
+        _run([hipcc, "-shared", "-fPIC", "--offload-arch=gfx950", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

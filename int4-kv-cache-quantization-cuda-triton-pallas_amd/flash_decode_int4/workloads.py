@@ -22,6 +22,8 @@ Named workloads (sizes of the reference's measurement plan):
   llama       B64 H32 D128 T4096, keys RoPE-rotated (base 10000, rotate-half
               pairing of channels d and d + D/2) at positions 0..T-1, then 4
               seeded channels per head scaled x20 (after rotation)
+  gqa         B8 Hkv8 Hq32 D128 T8192 (four query heads per kv-head; the
+              same key/value bytes as the anchor)
 
 ``backend="numpy"`` draws from ``np.random.RandomState(seed)`` (reproducible on
 any host); ``backend="torch"`` draws on the GPU from a seeded
@@ -43,6 +45,7 @@ WORKLOADS = {
     "sweep_32768": dict(batch=8, heads=32, head_dim=128, tokens=32768),
     "ragged": dict(batch=32, heads=32, head_dim=128, tokens="ragged", max_tokens=8192),
     "llama": dict(batch=64, heads=32, head_dim=128, tokens=4096, rope=True, outliers=4),
+    "gqa": dict(batch=8, heads=8, q_heads=32, head_dim=128, tokens=8192),
 }
 
 
@@ -84,11 +87,14 @@ def rope_rotate(k, base=10000.0):
 
 def make_workload(name=None, *, batch=None, heads=None, head_dim=None, tokens=None,
                   seq_lens=None, max_tokens=None, contiguous=False, rope=False, outliers=0,
-                  value_dtype="float32", seed=1234, backend="numpy", device="cuda"):
-    """Build a workload dict (see the module docstring for the layout)."""
+                  value_dtype="float32", seed=1234, backend="numpy", device="cuda",
+                  q_heads=None):
+    """Build a workload dict (see the module docstring for the layout); q has
+    q_heads heads (default: heads), q-head h reading kv-head h // (q_heads // heads)."""
     if name is not None:
         spec = dict(WORKLOADS[name])
         batch, heads, head_dim = spec["batch"], spec["heads"], spec["head_dim"]
+        q_heads = spec.get("q_heads", q_heads)
         tokens = spec["tokens"]
         max_tokens = spec.get("max_tokens", max_tokens)
         contiguous = spec.get("contiguous", contiguous)
@@ -102,12 +108,16 @@ def make_workload(name=None, *, batch=None, heads=None, head_dim=None, tokens=No
     seq_lens = np.asarray(seq_lens, dtype=np.int32)
     tmax = max(int(seq_lens.max(initial=0)), 1)
     table, P = page_layout(seq_lens, PAGE_ROWS, seed, contiguous)
-    out = dict(name=name, batch=batch, heads=heads, head_dim=head_dim, seq_lens=seq_lens,
+    q_heads = heads if q_heads is None else int(q_heads)
+    if q_heads % heads:
+        raise ValueError("q_heads must be a multiple of heads")
+    out = dict(name=name, batch=batch, heads=heads, q_heads=q_heads, head_dim=head_dim,
+               seq_lens=seq_lens,
                page_table=table, num_pages=P, page_rows=PAGE_ROWS, group_rows=GROUP_ROWS,
                max_tokens=tmax)
     if backend == "numpy":
         rng = np.random.RandomState(seed)
-        out["q"] = rng.randn(batch, heads, head_dim).astype(np.float32)
+        out["q"] = rng.randn(batch, q_heads, head_dim).astype(np.float32)
         k = rng.randn(batch, heads, tmax, head_dim).astype(np.float32)
         out["v_pages"] = rng.randn(P, heads, PAGE_ROWS, head_dim).astype(value_dtype)
         if rope:
@@ -123,7 +133,7 @@ def make_workload(name=None, *, batch=None, heads=None, head_dim=None, tokens=No
     dev = torch.device(device)
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
-    out["q"] = torch.randn(batch, heads, head_dim, generator=g, device=dev)
+    out["q"] = torch.randn(batch, q_heads, head_dim, generator=g, device=dev)
     k = torch.randn(batch, heads, tmax, head_dim, generator=g, device=dev)
     vdt = torch.float16 if value_dtype == "float16" else torch.float32
     out["v_pages"] = torch.randn(P, heads, PAGE_ROWS, head_dim, generator=g, device=dev).to(vdt)
@@ -145,20 +155,22 @@ def make_workload(name=None, *, batch=None, heads=None, head_dim=None, tokens=No
 
 
 def decode_bytes(seq_lens, heads, head_dim, value_bytes=4, page_rows=PAGE_ROWS,
-                 group_rows=GROUP_ROWS):
+                 group_rows=GROUP_ROWS, q_heads=None):
     """Algorithmic HBM bytes of one decode over valid tokens only.
 
-    Per (b, h): packed K T*D/2 + V T*D*value_bytes + scale and zp
+    Per (b, kv-head h): packed K T*D/2 + V T*D*value_bytes + scale and zp
     ceil(T/group)*D*8; per b: page table ceil(T/page_rows)*4 and seq_len 4;
-    plus q and the output, B*H*D*4 each. Split partials are excluded.
+    plus q and the output, B*Hq*D*4 each (Hq = q_heads, default heads).
+    Split partials are excluded.
     """
+    q_heads = heads if q_heads is None else q_heads
     total = 0
     for t in np.asarray(seq_lens, dtype=np.int64):
         t = int(t)
         g = (t + group_rows - 1) // group_rows
         total += heads * (t * head_dim // 2 + t * head_dim * value_bytes + g * head_dim * 8)
         total += ((t + page_rows - 1) // page_rows) * 4 + 4
-    total += 2 * len(seq_lens) * heads * head_dim * 4
+    total += 2 * len(seq_lens) * q_heads * head_dim * 4
     return total
 
 

@@ -289,3 +289,58 @@ class TestPagedDecode:
         a = _ops().flash_decode_paged(q_t, kp, v_t, s, z, pt, sl)
         b = _ops().flash_decode_paged(q_t, kp, v_t, s, z, pt, sl)
         assert bool((a == b).all())
+
+
+class TestGroupedQueryHeads:
+    """Several q-heads per kv-head: the grouped kernel serves 2, 4 or 8 heads
+    per workgroup (one read of the kv-head's pages for all of them); head
+    counts that no group size divides run the per-head kernel. Every case is
+    held to the oracle, whose q-head h reads kv-head h // (Hq / Hkv)."""
+
+    @pytest.mark.parametrize("D,rep,vdtype,lens,splits", [
+        (128, 4, "float32", [0, 37, 300, 2048], 0),
+        (128, 4, "float32", [700, 129], 3),
+        (128, 2, "float16", [1, 513, 1000], 0),
+        (64, 8, "float32", [16, 900], 0),
+        (64, 4, "float16", [257, 0, 60], 2),
+        (256, 4, "float32", [333, 1024], 0),
+        (256, 2, "float16", [129, 700], 0),
+        (128, 6, "float32", [400, 77], 0),   # groups of 2
+        (128, 3, "float32", [400, 77], 0),   # per-head kernel
+        (128, 8, "float32", [1200, 5], 0),   # groups of 4 at D=128
+    ])
+    def test_matches_oracle(self, D, rep, vdtype, lens, splits):
+        import torch
+        from flash_decode_int4.workloads import make_workload
+        hkv = 2
+        w = make_workload(batch=len(lens), heads=hkv, head_dim=D, seq_lens=lens, seed=D + rep)
+        vt = torch.float16 if vdtype == "float16" else None
+        q_t, kp, v_t, s, z, pt, sl = _paged_device(w, value_dtype=vt)
+        g = torch.Generator("cuda").manual_seed(rep)
+        q = torch.randn(len(lens), hkv * rep, D, device="cuda", generator=g)
+        out = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=splits)
+        out = out.cpu().numpy()
+        args = list(_oracle_inputs(w, kp, s, z, v=v_t.float().cpu().numpy()))
+        args[0] = q.cpu().numpy()
+        o32, o64 = paged_decode_ref(*args), paged_decode_f64(*args)
+        e32, eo = np.abs(out - o32).max(), np.abs(o32 - o64).max()
+        assert e32 <= max(TOL, 1.25 * eo), (e32, eo)
+        assert np.abs(out - o64).max() <= eo + 1e-6
+        empty = np.asarray(lens) == 0
+        assert np.all(out[empty] == 0.0)
+
+    def test_grouped_equals_per_head_kernel(self, monkeypatch):
+        """The grouped and the per-head kernel compute the same logits up to
+        fp64 rounding (other channel partitions per lane); the outputs agree to
+        float32 rounding."""
+        import torch
+        from flash_decode_int4.workloads import make_workload
+        w = make_workload(batch=2, heads=4, head_dim=128, seq_lens=[2048, 999], seed=21)
+        q_t, kp, v_t, s, z, pt, sl = _paged_device(w)
+        q = torch.randn(2, 16, 128, device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+        grouped = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=1)
+        monkeypatch.setenv("FDI4_DECODE_HEADS_PER_WG", "1")
+        per_head = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=1)
+        assert (grouped - per_head).abs().max().item() < 2e-6
+        again = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=1)
+        assert torch.equal(per_head, again)

@@ -225,15 +225,20 @@ class TestCABI:
         n = 8 * 32 * 4
         assert lib.fdi4_decode_workspace_bytes(8, 32, 128, 4) == n * 128 * 4 + n * 16
         assert lib.fdi4_decode_partials_bytes(8, 32, 128, 1) == 8 * 32 * (512 + 16)
-        # B8 x H32 fills the chip with 8-wave workgroups: one split, no merge.
-        cache = capi.PagedCache(max_pages=128, page_rows=16)
+        # B8 x H32 (one q-head per kv-head) fills the chip with 8-wave
+        # workgroups: one split, no merge.
+        cache = capi.PagedCache(max_pages=128, page_rows=16, num_kv_heads=32, head_dim=128)
         assert lib.fdi4_decode_num_splits(8, 32, cache) == 1
         # T=512 (32 chunks): still 8 waves of 4 chunks and one split.
-        cache = capi.PagedCache(max_pages=32, page_rows=16)
+        cache = capi.PagedCache(max_pages=32, page_rows=16, num_kv_heads=32, head_dim=128)
         assert lib.fdi4_decode_num_splits(8, 32, cache) == 1
         # B1 x H8 x 32768 tokens: 2048 chunks split 32 ways (2048 waves).
-        cache = capi.PagedCache(max_pages=2048, page_rows=16)
+        cache = capi.PagedCache(max_pages=2048, page_rows=16, num_kv_heads=8, head_dim=128)
         assert lib.fdi4_decode_num_splits(1, 8, cache) == 32
+        # GQA B8 x Hq32 x Hkv8 at D=128: four q-heads per workgroup, so 64
+        # workgroups of 8 waves and 4 splits for ~2048 waves.
+        cache = capi.PagedCache(max_pages=512, page_rows=16, num_kv_heads=8, head_dim=128)
+        assert lib.fdi4_decode_num_splits(8, 32, cache) == 4
 
     def test_invalid_arguments_are_rejected_before_any_device_call(self):
         from flash_decode_int4 import capi
