@@ -15,6 +15,11 @@ their own time to the GPU timeline); wall clock brackets the K steps too. Bytes 
 T*D*4, scale and zero-point ceil(T/128)*D*8 per (sequence, head), the page
 table, sequence lengths, q and the output.
 
+hbm_probe reports what a plain torch elementwise kernel reading and writing
+1 GiB reaches on the same box, beside the 8 TB/s specification used as the
+roofline peak; decode_us_median and quantizer_us_median are medians over
+blocks of 10 back-to-back launches.
+
 append_us times the decode-time append kernel (one token per (sequence,
 kv-head), open scale group re-quantized) on a cache of the workload's shape,
 at the first and at the last row of a group.
@@ -108,6 +113,49 @@ def build_sets(name, value_dtype, n_sets_hint=0, seq_lens=None):
     return sets, set_bytes
 
 
+def blocked_median_us(fn, n, block=10):
+    """Median over n // block blocks of the per-launch time of `block`
+    back-to-back launches (one event pair per block; each block starts from an
+    idle GPU, so this runs a little above the long-run mean)."""
+    import torch
+    out = []
+    for j in range(max(1, n // block)):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(block):
+            fn(j * block + i)
+        e1.record()
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) * 1e3 / block)
+    return median(out)
+
+
+def hbm_probes():
+    """Achievable bandwidth on this box with a plain torch elementwise kernel
+    that reads and writes 1 GiB."""
+    import torch
+    n = 2 ** 28
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+
+    def rate(fn, nbytes, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+
+    res = {"elementwise_copy_gbs": rate(lambda: torch.mul(a, 1.0, out=b), 2 * 4 * n)}
+    del a, b
+    torch.cuda.empty_cache()
+    return res
+
+
 def time_decode(sets, splits, steps, warmup):
     import torch
     from flash_decode_int4._lib import load_binding
@@ -156,13 +204,15 @@ def time_decode(sets, splits, steps, warmup):
     for i in range(warmup):
         step(i)
     out, wall, step_us = timed(step, steps)
+    step_median = blocked_median_us(step, steps)
     if S == 1:
         dec_us = step_us
     else:
         for i in range(warmup):
             decode_only(i)
         _, _, dec_us = timed(decode_only, steps)
-    return dict(splits=S, wall_s=wall, step_us=step_us, decode_us=dec_us,
+    return dict(splits=S, wall_s=wall, step_us=step_us, step_median_us=step_median,
+                decode_us=dec_us,
                 merge_us=max(step_us - dec_us, 0.0), last_out=out,
                 last_set=(steps - 1) % len(sets))
 
@@ -185,7 +235,7 @@ def time_quantizer(sets, steps, warmup):
         q(i)
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / steps
+    return e0.elapsed_time(e1) * 1e3 / steps, blocked_median_us(q, steps)
 
 
 def time_append(w, value_dtype, steps, warmup):
@@ -409,8 +459,9 @@ def main():
         sys.exit(1)
 
     res = time_decode(sets, args.splits, args.steps, args.warmup)
-    qt = time_quantizer(sets, args.steps, args.warmup)
+    qt, qt_median = time_quantizer(sets, args.steps, args.warmup)
     app = time_append(w0, args.value_dtype, args.steps, args.warmup)
+    probe = hbm_probes()
 
     # No shape specialization (the reference bench re-runs at seq_len + 1): every
     # length + 1, so pages end one row into a fresh page and groups one row into
@@ -452,13 +503,16 @@ def main():
             "input_sets": len(sets), "bytes_per_step": set_bytes,
         },
         "decode_us": round(step_us, 3),
+        "decode_us_median": round(res["step_median_us"], 3),
         "decode_kernel_us": round(dec_us, 3),
         "merge_us": round(mrg_us, 3),
         "hbm_frac": round(set_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "quantizer_us": round(q_us, 3),
+        "quantizer_us_median": round(qt_median, 3),
         "quantizer_gbs": round(qbytes / (q_us * 1e-6) / 1e9, 2),
         "quantizer_hbm_frac": round(qbytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "append_us": app,
+        "hbm_probe": probe,
         "checks": {
             "split_invariance_max_abs": gate,
             "seq_len_plus_1": {
