@@ -20,6 +20,10 @@ hbm_probe reports what a plain torch elementwise kernel reading and writing
 roofline peak; decode_us_median and quantizer_us_median are medians over
 blocks of 10 back-to-back launches.
 
+reference_config times the drop-in API (prepare_flash_decode_hip().run()) on
+the reference's own benchmark semantics, beside the reference's published
+CUDA time for it on other hardware (context, not vs_baseline).
+
 append_us times the decode-time append kernel (one token per (sequence,
 kv-head), open scale group re-quantized) on a cache of the workload's shape,
 at the first and at the last row of a group.
@@ -111,6 +115,44 @@ def build_sets(name, value_dtype, n_sets_hint=0, seq_lens=None):
         sets.append(s)
     torch.cuda.synchronize()
     return sets, set_bytes
+
+
+def time_reference_config(steps, warmup):
+    """The reference's own benchmark semantics through the drop-in API: B8 H32
+    D128 queries all attending one shared stream of 8 pages x 256 rows
+    (2048 tokens), each page one scale group with unpacked INT4 keys and fp32
+    values (reference benchmarks/bench_three_backend.py:113-129, src/ops.py
+    :176-253). Keys are quantized with this build's quantize_int4; run() of
+    prepare_flash_decode_hip is timed (inputs staged in HBM once)."""
+    import numpy as np
+    import torch
+    from flash_decode_int4 import ops
+    rng = np.random.RandomState(1234)
+    B, H, D, nb, bs = 8, 32, 128, 8, 256
+    query = rng.randn(B, H, D).astype(np.float32)
+    kq, ks, kz, vv = [], [], [], []
+    for _ in range(nb):
+        k = rng.randn(bs, D).astype(np.float32)
+        q, sc, zp = ops.quantize_int4(k, backend="hip")
+        kq.append(q); ks.append(sc); kz.append(zp)
+        vv.append(rng.randn(bs, D).astype(np.float32))
+    call = ops.prepare_flash_decode_hip(query, kq, ks, kz, vv)
+    for _ in range(warmup):
+        call.run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        out = call.run()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    return {"workload": "reference semantics: B8 H32 D128, one shared stream of 8 pages x "
+                        "256 rows (one scale group per page, unpacked INT4 keys, fp32 values)",
+            "decode_us": round(us, 3), "finite": bool(torch.isfinite(out).all()),
+            "reference_cuda_h100_us": 400.0,
+            "note": "the reference's published CUDA time for this configuration on an "
+                    "NVIDIA H100 (its README and results JSON); other hardware, context only"}
 
 
 def blocked_median_us(fn, n, block=10):
@@ -520,6 +562,7 @@ def main():
     qt, qt_median = time_quantizer(sets, args.steps, args.warmup)
     app = time_append(w0, args.value_dtype, args.steps, args.warmup)
     probe = hbm_probes()
+    refcfg = time_reference_config(args.steps, args.warmup)
 
     # No shape specialization (the reference bench re-runs at seq_len + 1): every
     # length + 1, so pages end one row into a fresh page and groups one row into
@@ -571,6 +614,7 @@ def main():
         "quantizer_hbm_frac": round(qbytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "append_us": app,
         "hbm_probe": probe,
+        "reference_config": refcfg,
         "checks": {
             "split_invariance_max_abs": gate,
             "seq_len_plus_1": {
