@@ -69,7 +69,30 @@ int pick_heads_per_wg(int d, int hq_per_kv) {
   return 1;
 }
 
+// Kernel family: with two or more q-heads per kv-head at D = 64 or 128 the
+// int8 matrix-core kernel (2, 4 or 8 heads per workgroup, 8 only at D=64;
+// B8 Hkv8 Hq32 T8192: 61 us against 75 us for the vector grouped kernel);
+// with one head per kv-head the vector per-head kernel, which is faster there
+// (anchor 51.9 against 54.2 us). FDI4_DECODE_MFMA=0 selects the vector
+// kernels throughout (tuning and A/B measurement).
+bool use_mfma(int d) {
+  const char* v = getenv("FDI4_DECODE_MFMA");
+  const bool on = !(v && v[0] == '0');
+  return on && (d == 64 || d == 128);
+}
+
+// Eight heads per workgroup fit the registers at D=64, and at D=128 with
+// float32 values (254 VGPRs); float16 values at D=128 stop at four.
+int pick_heads_per_wg_mfma(int d, int v_dtype, int hq_per_kv) {
+  const int fit = (d == 64 || v_dtype == FDI4_V_F32) ? 8 : 4;
+  const int cap = std::min(env_int("FDI4_DECODE_HEADS_PER_WG", 8), fit);
+  for (int hg : {8, 4, 2})
+    if (hg <= cap && hq_per_kv % hg == 0) return hg;
+  return 1;
+}
+
 struct DecodePlan {
+  int mfma;
   int heads_per_wg;
   int waves;
   int splits;
@@ -78,10 +101,13 @@ struct DecodePlan {
 // Launch shape of a decode: heads per workgroup, waves per workgroup (the
 // grouped kernel at D=256 has registers for four), and the split count that
 // gives about kTargetWaves waves over the (sequence, head group) streams.
-DecodePlan plan_decode(int batch, int hq, int hq_per_kv, int d, int chunks) {
+DecodePlan plan_decode(int batch, int hq, int hq_per_kv, int d, int v_dtype, int chunks) {
   DecodePlan p;
-  p.heads_per_wg = pick_heads_per_wg(d, hq_per_kv);
-  p.waves = (p.heads_per_wg > 1 && d == 256) ? 4 : pick_waves(chunks);
+  p.mfma = use_mfma(d) ? 1 : 0;
+  p.heads_per_wg = p.mfma ? pick_heads_per_wg_mfma(d, v_dtype, hq_per_kv)
+                          : pick_heads_per_wg(d, hq_per_kv);
+  if (p.heads_per_wg == 1) p.mfma = 0;
+  p.waves = (!p.mfma && p.heads_per_wg > 1 && d == 256) ? 4 : pick_waves(chunks);
   if (chunks <= 0) {
     p.splits = 1;
     return p;
@@ -297,7 +323,7 @@ int fdi4_decode_num_splits(int batch, int num_q_heads, const fdi4_paged_cache* c
       cache->num_kv_heads < 1 || num_q_heads % cache->num_kv_heads)
     return 1;
   return plan_decode(batch, num_q_heads, num_q_heads / cache->num_kv_heads, cache->head_dim,
-                     chunks_per_seq(cache))
+                     cache->v_dtype, chunks_per_seq(cache))
       .splits;
 }
 
@@ -329,6 +355,7 @@ namespace {
 // Validate and fill the kernel argument block shared by the decode entry points.
 hipError_t launch_decode_any(const DecodeArgs& a, int d, int v_dtype, int batch,
                              hipStream_t stream) {
+  if (a.mfma) return fdi4::launch_decode_mfma(a, d, v_dtype, batch, a.heads_per_wg, stream);
   if (a.heads_per_wg > 1)
     return fdi4::launch_decode_gqa(a, d, v_dtype, batch, a.heads_per_wg, stream);
   return fdi4::launch_decode(a, d, v_dtype, batch, stream);
@@ -345,7 +372,7 @@ int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_b
   if (cache->page_table && cache->pt_batch_stride < 0) return hipErrorInvalidValue;
   const int chunks = chunks_per_seq(cache);
   const DecodePlan plan = plan_decode(batch, num_q_heads, num_q_heads / cache->num_kv_heads,
-                                      cache->head_dim, chunks);
+                                      cache->head_dim, cache->v_dtype, chunks);
   int splits = num_splits > 0 ? num_splits : plan.splits;
   splits = std::max(1, std::min(splits, std::max(chunks, 1)));
   a->q = query;
@@ -385,6 +412,7 @@ int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_b
   a->final_out = 0;
   a->waves = plan.waves;
   a->heads_per_wg = plan.heads_per_wg;
+  a->mfma = plan.mfma;
   return hipSuccess;
 }
 
@@ -476,7 +504,7 @@ DenseLayout dense_layout(int B, int H, int D, int nb, int bs) {
     off += align_up((size_t)B * H * L.dp * sizeof(float));
   }
   // Every (sequence, head) attends the one shared page stream (kv-heads = 1).
-  L.splits = plan_decode(B, H, H, L.dp, nb * ceil_div(bs, 16)).splits;
+  L.splits = plan_decode(B, H, H, L.dp, FDI4_V_F32, nb * ceil_div(bs, 16)).splits;
   L.off_part = off;
   off += decode_ws_bytes(B, H, L.dp, L.splits);
   L.total = std::max<size_t>(off, kAlign);

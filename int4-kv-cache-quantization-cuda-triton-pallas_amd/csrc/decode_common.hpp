@@ -54,4 +54,18 @@ __device__ __forceinline__ ChunkMeta chunk_meta(const DecodeArgs& a, int b, int 
   return m;
 }
 
+// Valid rows of sequence b (every sequence spans max_pages pages when no
+// lengths are given).
+__device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
+  return a.seq_lens ? max(a.seq_lens[b], 0) : a.max_pages * a.page_rows;
+}
+
+// exp(x) for x <= ~0 in double: the exponent x*log2(e) is formed in double,
+// rounded once to float (relative 2^-24, so 6e-8 absolute where |x| < 1, where
+// the terms that matter lie) and raised with the hardware 2^y (v_exp_f32, ~1
+// ulp); -inf gives 0.
+__device__ __forceinline__ float exp2_of(double x) {
+  return __builtin_amdgcn_exp2f((float)(x * 1.4426950408889634));
+}
+
 }  // namespace fdi4

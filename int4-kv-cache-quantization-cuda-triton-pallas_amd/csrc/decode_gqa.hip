@@ -62,14 +62,6 @@ __device__ __forceinline__ void reduce_scatter(double* s, int lane) {
   }
 }
 
-// exp(x) for x <= ~0 in double: the exponent x*log2(e) is formed in double,
-// rounded once to float (relative 2^-24, so 6e-8 absolute where |x| < 1, where
-// the terms that matter lie) and raised with the hardware 2^y (v_exp_f32, ~1
-// ulp); -inf gives 0.
-__device__ __forceinline__ float exp2_of(double x) {
-  return __builtin_amdgcn_exp2f((float)(x * 1.4426950408889634));
-}
-
 template <int HG>
 struct HeadP {
   float p[HG];

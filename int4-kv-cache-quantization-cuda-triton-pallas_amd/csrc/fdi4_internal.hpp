@@ -65,6 +65,7 @@ struct DecodeArgs {
   int final_out;                        // 1: normalized output; 0: split partials
   int waves;                            // wave64s per workgroup (4 or 8)
   int heads_per_wg;                     // q-heads per workgroup (1: per-head kernel)
+  int mfma;                             // int8 matrix-core kernel (D = 64 or 128)
   float* out;
   int64_t o_b, o_h;
   float* ws_acc;                        // [B, Hq, S, D]
@@ -89,6 +90,9 @@ hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hip
 
 hipError_t launch_decode_gqa(const DecodeArgs& a, int D, int v_dtype, int batch, int hg,
                              hipStream_t st);
+
+hipError_t launch_decode_mfma(const DecodeArgs& a, int D, int v_dtype, int batch, int hg,
+                              hipStream_t st);
 
 hipError_t launch_merge(const float* ws_acc, const double* ws_ml, int batch, int hq, int D,
                         int splits, float* out, int64_t o_b, int64_t o_h, hipStream_t st);

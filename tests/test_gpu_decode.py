@@ -329,6 +329,21 @@ class TestGroupedQueryHeads:
         empty = np.asarray(lens) == 0
         assert np.all(out[empty] == 0.0)
 
+    @pytest.mark.parametrize("D,rep", [(128, 4), (64, 8), (128, 2), (128, 8)])
+    def test_matrix_core_equals_vector_kernel(self, monkeypatch, D, rep):
+        """The int8 matrix-core kernel's logits are exact up to the 41-bit
+        rounding of q*s; it agrees with the vector grouped kernel (fp64
+        products) to float32 rounding."""
+        import torch
+        from flash_decode_int4.workloads import make_workload
+        w = make_workload(batch=2, heads=2, head_dim=D, seq_lens=[1500, 333], seed=D + rep)
+        q_t, kp, v_t, s, z, pt, sl = _paged_device(w)
+        q = torch.randn(2, 2 * rep, D, device="cuda", generator=torch.Generator("cuda").manual_seed(7))
+        mfma = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=2)
+        monkeypatch.setenv("FDI4_DECODE_MFMA", "0")
+        vec = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=2)
+        assert (mfma - vec).abs().max().item() < 2e-6
+
     def test_grouped_equals_per_head_kernel(self, monkeypatch):
         """The grouped and the per-head kernel compute the same logits up to
         fp64 rounding (other channel partitions per lane); the outputs agree to
