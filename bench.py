@@ -24,6 +24,10 @@ reference_config times the drop-in API (prepare_flash_decode_hip().run()) on
 the reference's own benchmark semantics, beside the reference's published
 CUDA time for it on other hardware (context, not vs_baseline).
 
+fake_quant times the quality-study kernel (INT4 quantize-dequantize of a key
+tensor in blocks) on a Llama-2-7B-sized perplexity window and on the decode
+workload's keys, beside the same computation as eager torch operations.
+
 append_us times the decode-time append kernel (one token per (sequence,
 kv-head), open scale group re-quantized) on a cache of the workload's shape,
 at the first and at the last row of a group.
@@ -325,6 +329,82 @@ def time_append(w, value_dtype, steps, warmup):
     return out
 
 
+def _torch_chain_fake_quant(k, block):
+    """The harness's fake quantization (scripts/validate_llama.py:126-154) as
+    a chain of eager torch operations, timed as the unfused baseline: upcast,
+    pad the last block with its last row, per-block extremes, bins, dequantize,
+    cast back."""
+    import torch
+    b, h, s, d = k.shape
+    nb = -(-s // block)
+    x = k.float()
+    if nb * block != s:
+        x = torch.cat([x, x[:, :, -1:].expand(b, h, nb * block - s, d)], dim=2)
+    x = x.view(b, h, nb, block, d)
+    lo = x.amin(dim=3, keepdim=True)
+    step = (x.amax(dim=3, keepdim=True) - lo).clamp_min(1e-8) / 15.0
+    q = torch.floor((x - lo) / step + 0.5).clamp_(0.0, 15.0)
+    return (q * step + lo).view(b, h, nb * block, d)[:, :, :s].to(k.dtype)
+
+
+def time_fake_quant(steps, warmup):
+    """Device fake quantization of keys (quality-study path) on two shapes:
+    one perplexity window of a Llama-2-7B-sized model (32 kv-heads x 2048
+    positions x 128, float16, 256-position blocks, the harness defaults) and
+    the decode workload's key tensor (8 x 32 x 2048 x 128 float32, 128-position
+    blocks). Inputs rotate over enough sets to exceed twice the Infinity Cache;
+    bytes are one read and one write of the keys. The harness window is also
+    timed as an eager chain of torch operations (the unfused formulation)."""
+    import torch
+    from flash_decode_int4.quality import fake_quantize_keys
+    out = {}
+    cases = (("harness_window_f16", (1, 32, 2048, 128), torch.float16, 256),
+             ("decode_keys_f32", (8, 32, 2048, 128), torch.float32, 128))
+    for name, shape, dt, block in cases:
+        nbytes = 2 * math.prod(shape) * torch.empty(0, dtype=dt).element_size()
+        n_sets = max(2, math.ceil(2 * INFINITY_CACHE / nbytes))
+        g = torch.Generator(device="cuda")
+        g.manual_seed(91)
+        ks = [torch.randn(shape, generator=g, device="cuda").to(dt) for _ in range(n_sets)]
+        outs = [torch.empty_like(k) for k in ks]
+        # Eager torch divides by the Python scalar 15.0 through its float32
+        # reciprocal: the kernel's reciprocal scale form reproduces it bit for bit.
+        ok = bool(torch.equal(fake_quantize_keys(ks[0], block, scale_op="reciprocal"),
+                              _torch_chain_fake_quant(ks[0], block)))
+
+        def fq(i):
+            fake_quantize_keys(ks[i % n_sets], block, out=outs[i % n_sets])
+
+        for i in range(warmup):
+            fq(i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(steps):
+            fq(i)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        rec = {"shape": list(shape), "dtype": str(dt).replace("torch.", ""), "block": block,
+               "us": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+               "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+               "reciprocal_form_equals_torch_chain": ok}
+        if name == "harness_window_f16":
+            for i in range(warmup):
+                _torch_chain_fake_quant(ks[i % n_sets], block)
+            torch.cuda.synchronize()
+            e0.record()
+            for i in range(steps):
+                _torch_chain_fake_quant(ks[i % n_sets], block)
+            e1.record()
+            torch.cuda.synchronize()
+            rec["torch_chain_us"] = round(e0.elapsed_time(e1) * 1e3 / steps, 3)
+        out[name] = rec
+        del ks, outs
+        torch.cuda.empty_cache()
+    return out
+
+
 def median(x):
     s = sorted(x)
     n = len(s)
@@ -523,6 +603,19 @@ def pmc_traffic(args):
             "write_factor_bytes_per_unit": copy_bytes / out["WRITE_SIZE"][1]}, None
 
 
+def decode_kernel_label(w, value_dtype):
+    """The decode kernel the library's planner picks for this workload: the
+    per-head kernel for one q-head per kv-head, the int8 matrix-core kernel
+    for grouped heads at head_dim 64 / 128 (unless FDI4_DECODE_MFMA=0), the
+    vector grouped kernel otherwise."""
+    d, rep = w["head_dim"], w["q_heads"] // w["heads"]
+    if rep == 1:
+        return f"decode_kernel<D={d}, {value_dtype} values>"
+    kind = ("decode_mfma_kernel" if d in (64, 128) and os.environ.get("FDI4_DECODE_MFMA") != "0"
+            else "decode_gqa_kernel")
+    return f"{kind}<D={d}, {value_dtype} values, {rep} q-heads per kv-head>"
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -563,6 +656,7 @@ def main():
     app = time_append(w0, args.value_dtype, args.steps, args.warmup)
     probe = hbm_probes()
     refcfg = time_reference_config(args.steps, args.warmup)
+    fq = time_fake_quant(args.steps, args.warmup)
 
     # No shape specialization (the reference bench re-runs at seq_len + 1): every
     # length + 1, so pages end one row into a fresh page and groups one row into
@@ -615,6 +709,7 @@ def main():
         "append_us": app,
         "hbm_probe": probe,
         "reference_config": refcfg,
+        "fake_quant": fq,
         "checks": {
             "split_invariance_max_abs": gate,
             "seq_len_plus_1": {
@@ -629,10 +724,7 @@ def main():
             "unit": "GB/s",
             "frac": round(set_bytes / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": (f"decode_kernel<D={w0['head_dim']}, {args.value_dtype} values>"
-                       if w0["q_heads"] == w0["heads"] else
-                       f"decode_gqa_kernel<D={w0['head_dim']}, {args.value_dtype} values, "
-                       f"{w0['q_heads'] // w0['heads']} q-heads per kv-head>"),
+            "kernel": decode_kernel_label(w0, args.value_dtype),
         },
     }
     if not args.no_pmc:

@@ -26,6 +26,9 @@ extern "C" {
 #define FDI4_ABI_VERSION 1
 
 enum fdi4_value_dtype { FDI4_V_F32 = 0, FDI4_V_F16 = 1 };
+enum fdi4_key_dtype { FDI4_K_F32 = 0, FDI4_K_F16 = 1, FDI4_K_BF16 = 2 };
+enum fdi4_rounding { FDI4_ROUND_HALF_UP = 0, FDI4_ROUND_HALF_EVEN = 1 };
+enum fdi4_scale_op { FDI4_SCALE_DIVIDE = 0, FDI4_SCALE_RECIPROCAL = 1 };
 
 /* Device layout of a paged INT4 key/value cache.
  *
@@ -204,6 +207,33 @@ int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
 int fdi4_merge_splits(const float* part_acc, const double* part_ml, int batch, int num_q_heads,
                       int head_dim, int num_splits, float* out, int64_t out_batch_stride,
                       int64_t out_head_stride, hipStream_t stream);
+
+/* INT4 quantize-dequantize ("fake quantization") of keys k[b, h, t, :]
+ * (b < batch, h < heads, t < seq_len; element strides, channel stride 1) into
+ * out (same dtype, its own element strides): per (sequence, head, block of
+ * block_size positions, channel) over the block's valid rows, mn/mx,
+ * scale = max(mx - mn, 1e-8f) / 15 (FDI4_SCALE_DIVIDE, IEEE division, as
+ * NumPy and torch on the CPU evaluate the reference's formula) or
+ * max(mx - mn, 1e-8f) * float(1/15) (FDI4_SCALE_RECIPROCAL, as eager torch on
+ * a GPU evaluates it: a tensor divided by a Python scalar is multiplied by
+ * the reciprocal), and
+ *   FDI4_ROUND_HALF_UP:   q = clamp(floor((x - mn) / scale + 0.5), 0, 15),
+ *                         out = q*scale + mn
+ *   FDI4_ROUND_HALF_EVEN: q = clamp(rint((x - mn) / scale), 0, 15),
+ *                         zp = -mn / scale, out = q*scale - zp*scale
+ * in float32 (one rounding per operation), converted to the key dtype
+ * (FDI4_K_F32 / F16 / BF16) with round-to-nearest-even. Finite keys only.
+ * head_dim * element size is a multiple of 16 bytes and head_dim <= 512; k,
+ * out and their strides are 16-byte aligned; block_size >= 1; heads and
+ * batch <= 65535. out must not overlap k. Half-up is fake_quantize_keys of
+ * the reference's quality study (scripts/validate_llama.py:126-154);
+ * half-even is its stored scheme, quantize_and_dequantize_ref
+ * (src/quantize_int4_ref.py:139-158), per block. */
+int fdi4_fake_quantize(const void* k, int key_dtype, int batch, int heads, int seq_len,
+                       int head_dim, int64_t k_batch_stride, int64_t k_head_stride,
+                       int64_t k_row_stride, void* out, int64_t out_batch_stride,
+                       int64_t out_head_stride, int64_t out_row_stride, int block_size,
+                       int rounding, int scale_op, hipStream_t stream);
 
 /* Device nibble packing: out[r, j] = q[r, 2j] | q[r, 2j+1] << 4 for
  * j < ceil(C/2) (odd C zero-padded), zero for ceil(C/2) <= j < out_cols.

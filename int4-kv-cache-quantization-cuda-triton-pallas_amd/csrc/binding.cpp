@@ -423,6 +423,37 @@ torch::Tensor pack_int4(torch::Tensor q, int64_t out_cols) {
   return out;
 }
 
+// INT4 quantize-dequantize of keys [batch, heads, seq, head_dim] into `out`
+// (same dtype and shape; see fdi4_fake_quantize). rounding: 0 half-up, 1
+// half-even; scale_op: 0 divide, 1 reciprocal.
+void fake_quantize(torch::Tensor k, torch::Tensor out, int64_t block_size, int64_t rounding,
+                   int64_t scale_op) {
+  CHECK_DEV(k);
+  CHECK_DEV(out);
+  TORCH_CHECK(k.dim() == 4, "k must be 4D [batch, heads, seq, head_dim], got ", k.dim(), "D");
+  const auto dt = k.scalar_type();
+  int code;
+  if (dt == torch::kFloat32) code = FDI4_K_F32;
+  else if (dt == torch::kFloat16) code = FDI4_K_F16;
+  else if (dt == torch::kBFloat16) code = FDI4_K_BF16;
+  else TORCH_CHECK(false, "k must be float32, float16 or bfloat16, got ", dt);
+  TORCH_CHECK(out.scalar_type() == dt && out.sizes() == k.sizes(),
+              "out must have the dtype and shape of k");
+  TORCH_CHECK(k.stride(3) == 1 && out.stride(3) == 1, "k and out need contiguous rows");
+  TORCH_CHECK(block_size >= 1 && block_size <= INT32_MAX, "block_size must be >= 1");
+  TORCH_CHECK(rounding == FDI4_ROUND_HALF_UP || rounding == FDI4_ROUND_HALF_EVEN,
+              "rounding must be 0 (half-up) or 1 (half-even)");
+  TORCH_CHECK(scale_op == FDI4_SCALE_DIVIDE || scale_op == FDI4_SCALE_RECIPROCAL,
+              "scale_op must be 0 (divide) or 1 (reciprocal)");
+  TORCH_CHECK(k.size(0) <= 65535 && k.size(1) <= 65535 && k.size(2) <= INT32_MAX,
+              "k has too many sequences, heads or positions");
+  check_rc(fdi4_fake_quantize(k.data_ptr(), code, (int)k.size(0), (int)k.size(1), (int)k.size(2),
+                              (int)k.size(3), k.stride(0), k.stride(1), k.stride(2),
+                              out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+                              (int)block_size, (int)rounding, (int)scale_op, stream()),
+           "fake_quantize");
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -441,5 +472,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_partials_bytes", &decode_partials_bytes, "Bytes of the split partials");
   m.def("decode_num_splits", &decode_num_splits, "Split count chosen for a decode shape");
   m.def("pack_int4", &pack_int4, "Device nibble packing (HIP)");
+  m.def("fake_quantize", &fake_quantize, "INT4 quantize-dequantize of keys in blocks (HIP)");
   m.def("abi_version", &fdi4_abi_version, "C ABI version of the loaded libfdi4");
 }

@@ -617,6 +617,46 @@ int fdi4_flash_decode_int4(const float* query, const uint8_t* k_q, const float* 
   return rc != hipSuccess ? rc : f;
 }
 
+int fdi4_fake_quantize(const void* k, int key_dtype, int batch, int heads, int seq_len,
+                       int head_dim, int64_t k_batch_stride, int64_t k_head_stride,
+                       int64_t k_row_stride, void* out, int64_t out_batch_stride,
+                       int64_t out_head_stride, int64_t out_row_stride, int block_size,
+                       int rounding, int scale_op, hipStream_t stream) {
+  if (key_dtype != FDI4_K_F32 && key_dtype != FDI4_K_F16 && key_dtype != FDI4_K_BF16)
+    return hipErrorInvalidValue;
+  if (rounding != FDI4_ROUND_HALF_UP && rounding != FDI4_ROUND_HALF_EVEN)
+    return hipErrorInvalidValue;
+  if (scale_op != FDI4_SCALE_DIVIDE && scale_op != FDI4_SCALE_RECIPROCAL)
+    return hipErrorInvalidValue;
+  if (batch < 0 || heads < 0 || seq_len < 0 || batch > 65535 || heads > 65535 ||
+      block_size < 1 || head_dim < 1 || head_dim > fdi4::fake_quant_max_head_dim())
+    return hipErrorInvalidValue;
+  if (batch == 0 || heads == 0 || seq_len == 0) return hipSuccess;
+  if (!k || !out) return hipErrorInvalidValue;
+  const int64_t esz = key_dtype == FDI4_K_F32 ? 4 : 2;
+  // 16-byte vector loads and stores of whole row pieces.
+  if ((head_dim * esz) % 16 || !aligned(k, 16) || !aligned(out, 16) ||
+      (k_batch_stride * esz) % 16 || (k_head_stride * esz) % 16 || (k_row_stride * esz) % 16 ||
+      (out_batch_stride * esz) % 16 || (out_head_stride * esz) % 16 ||
+      (out_row_stride * esz) % 16)
+    return hipErrorInvalidValue;
+  fdi4::FakeQuantArgs a;
+  a.k = static_cast<const uint8_t*>(k);
+  a.k_b = k_batch_stride * esz;
+  a.k_h = k_head_stride * esz;
+  a.k_t = k_row_stride * esz;
+  a.out = static_cast<uint8_t*>(out);
+  a.o_b = out_batch_stride * esz;
+  a.o_h = out_head_stride * esz;
+  a.o_t = out_row_stride * esz;
+  a.seq_len = seq_len;
+  a.head_dim = head_dim;
+  a.block = block_size;
+  a.scale_recip = scale_op == FDI4_SCALE_RECIPROCAL ? 1 : 0;
+  a.nsplit = a.cw = a.vpr = a.rpp = 0;
+  return fdi4::launch_fake_quant(a, key_dtype, rounding, batch, heads, stream);
+}
+
 int fdi4_pack_int4(const uint8_t* q, int64_t rows, int num_channels, int64_t q_row_stride,
                    uint8_t* out, int64_t out_row_stride, int out_cols, hipStream_t stream) {
   if (!q || !out || rows < 0 || num_channels <= 0) return hipErrorInvalidValue;

@@ -72,6 +72,20 @@ struct DecodeArgs {
   double* ws_ml;                        // [B, Hq, S, 2] = (m, l)
 };
 
+// Quantize-dequantize of keys [B, H, T, D] (channel stride 1) in blocks of
+// `block` positions into out (same type and shape, own strides).
+struct FakeQuantArgs {
+  const uint8_t* k;
+  int64_t k_b, k_h, k_t;                // bytes
+  uint8_t* out;
+  int64_t o_b, o_h, o_t;                // bytes
+  int seq_len, head_dim, block;
+  int scale_recip;                      // 1: scale = span * (1/15); 0: span / 15
+  // Set by the launcher: channel slices per block, channels per slice,
+  // 16-byte vectors per slice row, rows per sweep.
+  int nsplit, cw, vpr, rpp;
+};
+
 hipError_t launch_quantize_rows(const float* kv, int64_t rows, int C, int64_t stride, uint8_t* q,
                                 int64_t q_stride, bool packed, float* scale_out, float* zp_out,
                                 void* ws, hipStream_t st);
@@ -96,6 +110,10 @@ hipError_t launch_decode_mfma(const DecodeArgs& a, int D, int v_dtype, int batch
 
 hipError_t launch_merge(const float* ws_acc, const double* ws_ml, int batch, int hq, int D,
                         int splits, float* out, int64_t o_b, int64_t o_h, hipStream_t st);
+
+hipError_t launch_fake_quant(const FakeQuantArgs& a, int key_dtype, int rounding, int batch,
+                             int heads, hipStream_t st);
+int fake_quant_max_head_dim();
 
 hipError_t launch_pad_rows(const float* src, int64_t rows, int cols, int64_t s_stride, float* dst,
                            int64_t d_stride, int d_cols, hipStream_t st);

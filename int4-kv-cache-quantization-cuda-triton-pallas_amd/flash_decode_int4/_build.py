@@ -25,7 +25,8 @@ CSRC = os.path.join(ROOT_DIR, "csrc")
 INCLUDE = os.path.join(os.path.dirname(ROOT_DIR), "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_SOURCES = ("quantize.hip", "decode.hip", "decode_gqa.hip", "decode_mfma.hip", "capi.hip")
+HIP_SOURCES = ("quantize.hip", "decode.hip", "decode_gqa.hip", "decode_mfma.hip", "fake_quant.hip",
+               "capi.hip")
 LIB_PATH = os.path.join(PKG_DIR, "libfdi4.so")
 EXT_PATH = os.path.join(PKG_DIR, "_C.so")
 

@@ -15,6 +15,9 @@ c_int, c_int32, c_int64, c_size_t, c_void_p = (ctypes.c_int, ctypes.c_int32, cty
 
 V_F32 = 0
 V_F16 = 1
+K_F32, K_F16, K_BF16 = 0, 1, 2
+ROUND_HALF_UP, ROUND_HALF_EVEN = 0, 1
+SCALE_DIVIDE, SCALE_RECIPROCAL = 0, 1
 
 
 class PagedCache(ctypes.Structure):
@@ -77,6 +80,9 @@ SIGNATURES = {
                                   c_int64, c_int64, c_void_p]),
     "fdi4_pack_int4": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_int64, c_int,
                                c_void_p]),
+    "fdi4_fake_quantize": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int64,
+                                   c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int,
+                                   c_int, c_int, c_void_p]),
 }
 
 _lib = None

@@ -15,6 +15,9 @@ quantize   per-channel asymmetric INT4 quantizer, dequantizer, nibble packing
 attention  page-loop online softmax (reference src/flash_decode_ref.py:30-223),
            the float64 arbiter (reference tests/test_pallas_flash_decode.py:53-78)
            and the per-(sequence, kv-head) paged construction
+fakequant  quantize-dequantize of key tensors in blocks (reference
+           scripts/validate_llama.py:126-154; half-even form per block of
+           src/quantize_int4_ref.py:139-158) and the bfloat16 rounding
 cref       ctypes loader for the C restatement in ``oracle/c`` (quantizer,
            packing and a float64 attention arbiter), built by ``oracle/Makefile``
 
@@ -40,4 +43,9 @@ from .attention import (  # noqa: F401
     float32_floor,
     paged_decode_ref,
     paged_decode_f64,
+)
+from .fakequant import (  # noqa: F401
+    fake_quantize_keys_ref,
+    bf16_bits,
+    bf16_bits_to_f32,
 )

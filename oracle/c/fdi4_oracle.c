@@ -10,6 +10,10 @@
  *                           round-to-nearest-even mode) -- an implementation
  *                           independent of NumPy's vectorized one.
  *   oracle_pack             reference src/int4_pack.py:14-29
+ *   oracle_fake_quantize    reference scripts/validate_llama.py:126-154 (and,
+ *                           with rounding 1, src/quantize_int4_ref.py:139-158
+ *                           per block) for one key stream [rows, C].
+ *   oracle_f32_to_bf16      round-to-nearest-even float32 -> bfloat16 bits.
  *   oracle_paged_attention_f64
  *                           the float64 arbiter (reference
  *                           tests/test_pallas_flash_decode.py:53-78) over the
@@ -23,6 +27,7 @@
 #include <stddef.h>
 #include <stdint.h>
 #include <stdlib.h>
+#include <string.h>
 
 void oracle_quantize_group(const float* x, int rows, int C, int64_t stride, uint8_t* q,
                            int64_t q_stride, float* scale, float* zp) {
@@ -57,6 +62,58 @@ void oracle_pack(const uint8_t* q, int64_t rows, int C, uint8_t* out) {
       const unsigned hi = (2 * j + 1 < C) ? q[r * C + 2 * j + 1] : 0u;
       out[r * pc + j] = (uint8_t)(lo | (hi << 4));
     }
+}
+
+/* Quantize-dequantize of x [rows, C] (contiguous) in blocks of `block` rows:
+ * rounding 0 = floor(t + 0.5f) with dq = q*s + mn, rounding 1 = rintf(t) with
+ * dq = q*s - zp*s, t = (x - mn) / s, s = max(mx - mn, 1e-8f) / 15 (recip = 0)
+ * or max(mx - mn, 1e-8f) * float(1/15) (recip = 1). */
+void oracle_fake_quantize(const float* x, int rows, int C, int block, int rounding, int recip,
+                          float* out) {
+  const volatile float fifteen = 15.0f;
+  const float r15 = 1.0f / fifteen; /* float32(1/15), rounded at run time */
+  for (int r0 = 0; r0 < rows; r0 += block) {
+    const int n = rows - r0 < block ? rows - r0 : block;
+    for (int c = 0; c < C; ++c) {
+      float mn = x[(int64_t)r0 * C + c], mx = mn;
+      for (int r = 1; r < n; ++r) {
+        const float v = x[(int64_t)(r0 + r) * C + c];
+        if (v < mn) mn = v;
+        if (v > mx) mx = v;
+      }
+      float span = mx - mn;
+      if (span < 1e-8f) span = 1e-8f;
+      const float s = recip ? span * r15 : span / 15.0f;
+      const float z = (-mn) / s;
+      for (int r = 0; r < n; ++r) {
+        const int64_t i = (int64_t)(r0 + r) * C + c;
+        const float t = (x[i] - mn) / s;
+        float q = rounding == 0 ? floorf(t + 0.5f) : rintf(t);
+        if (q < 0.0f) q = 0.0f;
+        if (q > 15.0f) q = 15.0f;
+        if (rounding == 0) {
+          const float qs = q * s;
+          out[i] = qs + mn;
+        } else {
+          const float qs = q * s, zs = z * s;
+          out[i] = qs - zs;
+        }
+      }
+    }
+  }
+}
+
+void oracle_f32_to_bf16(const float* x, int64_t n, uint16_t* out) {
+  for (int64_t i = 0; i < n; ++i) {
+    uint32_t u;
+    memcpy(&u, &x[i], 4);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) {
+      out[i] = 0x7FC0u;
+      continue;
+    }
+    /* Ties go to the even upper half: add 0x7FFF plus the upper half's low bit. */
+    out[i] = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+  }
 }
 
 /* query [B, Hq, D]; k_pages [P, Hkv, R, D/2]; v_pages [P, Hkv, R, D] float;

@@ -29,6 +29,9 @@ def load():
         lib.oracle_paged_attention_f64.argtypes = [
             P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_int, ctypes.c_int, P, P,
             ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P]
+        lib.oracle_fake_quantize.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_int, ctypes.c_int, P]
+        lib.oracle_f32_to_bf16.argtypes = [P, ctypes.c_int64, P]
         _lib = lib
     return _lib
 
@@ -73,4 +76,21 @@ def paged_attention_f64(query, k_pages, v_pages, k_scale, k_zp, page_table, seq_
         _p(query), B, Hq, D, _p(k_pages), _p(v_pages), Hkv, R, _p(k_scale), _p(k_zp),
         k_scale.shape[2], _p(page_table), page_table.shape[1], _p(seq_lens),
         group_rows // page_rows, _p(out))
+    return out
+
+
+def fake_quantize(x, block, rounding, recip=0):
+    """Quantize-dequantize of one stream x [rows, C] in blocks (rounding 0
+    half-up, 1 half-even; recip 1 for the reciprocal scale)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, c = x.shape
+    out = np.zeros_like(x)
+    load().oracle_fake_quantize(_p(x), rows, c, int(block), int(rounding), int(recip), _p(out))
+    return out
+
+
+def f32_to_bf16_bits(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.shape, np.uint16)
+    load().oracle_f32_to_bf16(_p(x), x.size, _p(out))
     return out
