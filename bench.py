@@ -36,10 +36,11 @@ The cpu_baseline leg times the NumPy oracle (the reference's page loop, one
 call per (sequence, head) stream, one BLAS thread) on this host's cores over
 the same workload and uses its output as the parity check of the GPU result.
 
-The HBM traffic of the decode kernel comes from two rocprofv3 --pmc child
-runs (FETCH_SIZE, then WRITE_SIZE), each calibrated by the same counter on a
-256 MiB elementwise kernel; --no-pmc skips them (and must be given when this
-script itself runs under rocprofv3).
+The HBM traffic of the decode kernel (and of the fake-quantization kernel)
+comes from two rocprofv3 --pmc child runs (FETCH_SIZE, then WRITE_SIZE), each
+calibrated by the same counter on a kernel that moves 256 MiB in that
+direction only (a sum for reads, a fill for writes); --no-pmc skips them (and
+must be given when this script itself runs under rocprofv3).
 
 Prints ONE JSON line. Options: --workload (anchor, sweep_512 ... llama,
 ragged), --splits, --value-dtype float16, --no-cpu, --no-pmc.
@@ -63,6 +64,8 @@ if PKG_ROOT not in sys.path:
 METRIC = ("fused INT4 decode attn µs + % HBM peak @B8×H32×D128×2048; "
           "quantizer GB/s")
 HBM_PEAK_GBS = 8000.0
+#: Decode kernel families (the planner picks one per shape).
+DECODE_KERNELS = ("decode_kernel", "decode_gqa_kernel", "decode_mfma_kernel")
 INFINITY_CACHE = 256 * 2 ** 20
 
 
@@ -386,7 +389,7 @@ def time_fake_quant(steps, warmup):
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / steps
         rec = {"shape": list(shape), "dtype": str(dt).replace("torch.", ""), "block": block,
-               "us": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+               "bytes": nbytes, "us": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
                "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                "reciprocal_form_equals_torch_chain": ok}
         if name == "harness_window_f16":
@@ -544,24 +547,36 @@ def cpu_baseline(st, gpu_out, runs, vbytes):
 
 def pmc_child(args):
     """Run a few decode and quantizer launches on one set (for rocprofv3
-    --pmc); also a 256 MiB device copy whose counters calibrate the
-    bytes/counter factor."""
+    --pmc), the calibration kernels (256 MiB fill, sum and copy) whose
+    counters give the bytes/counter factors, then the fake-quantization
+    workloads."""
     import torch
     sets, _ = build_sets(args.workload, args.value_dtype, n_sets_hint=1)
     r = time_decode(sets, args.splits, steps=3, warmup=1)
     time_quantizer(sets, steps=3, warmup=1)
+    del sets
+    torch.cuda.empty_cache()
+    # Calibration kernels over 256 MiB of float32: a fill (writes only), a sum
+    # (reads only) and an elementwise copy (reads and writes).
     a = torch.empty(64 * 2 ** 20, dtype=torch.float32, device="cuda")
     b = torch.empty_like(a)
-    a.fill_(1.0)
     for _ in range(3):
-        torch.mul(a, 1.0, out=b)  # an elementwise kernel: reads 256 MiB, writes 256 MiB
+        a.fill_(1.0)
+    for _ in range(3):
+        torch.sum(a)
+    for _ in range(3):
+        torch.mul(a, 1.0, out=b)
     torch.cuda.synchronize()
+    del a, b
+    torch.cuda.empty_cache()
+    time_fake_quant(steps=2, warmup=1)
     print(json.dumps({"splits": r["splits"]}))
 
 
 def pmc_traffic(args):
     """HBM bytes per decode-kernel launch from FETCH_SIZE and WRITE_SIZE passes,
-    each scaled by the same counter's reading for a 256 MiB copy kernel."""
+    each scaled by the same counter's reading for a kernel that moves 256 MiB
+    in that direction only; also the fake-quantization kernel's bytes."""
     exe = shutil.which("rocprofv3")
     if exe is None:
         return None, "rocprofv3 not found"
@@ -584,23 +599,37 @@ def pmc_traffic(args):
                 if f.endswith("counter_collection.csv"):
                     with open(os.path.join(dirpath, f)) as fh:
                         rows += list(csv.DictReader(fh))
-        dec = [float(r["Counter_Value"]) for r in rows
-               if "decode_kernel" in r.get("Kernel_Name", "")
-               and r.get("Counter_Name") == counter]
-        cpy = [float(r["Counter_Value"]) for r in rows
-               if "MulFunctor" in r.get("Kernel_Name", "")
-               and r.get("Counter_Name") == counter]
+        def values(pred):
+            return [float(r["Counter_Value"]) for r in rows
+                    if pred(r.get("Kernel_Name", "")) and r.get("Counter_Name") == counter]
+
+        dec = values(lambda k: any(f"{n}<" in k for n in DECODE_KERNELS))
+        # The calibration kernel for this counter: reads only for FETCH_SIZE
+        # (the sum), writes only for WRITE_SIZE (the fill).
+        cal = values(lambda k: ("sum_functor" in k) if counter == "FETCH_SIZE"
+                     else ("FillFunctor" in k))
+        cpy = values(lambda k: "MulFunctor" in k)
+        fq = {name: values(lambda k, t=tag: "fake_quant_kernel" in k and t in k)
+              for name, tag in (("harness_window_f16", "F16Key"), ("decode_keys_f32", "F32Key"))}
         shutil.rmtree(d, ignore_errors=True)
-        if not dec or not cpy:
-            return None, f"no {counter} rows for the decode or copy kernel"
-        out[counter] = (median(dec), max(cpy))
-    # A 256 MiB copy reads and writes 256 MiB: the factor converts counter units to bytes.
-    copy_bytes = 256 * 2 ** 20
-    fetch = out["FETCH_SIZE"][0] * copy_bytes / out["FETCH_SIZE"][1]
-    write = out["WRITE_SIZE"][0] * copy_bytes / out["WRITE_SIZE"][1]
-    return {"fetch_bytes": fetch, "write_bytes": write,
-            "fetch_factor_bytes_per_unit": copy_bytes / out["FETCH_SIZE"][1],
-            "write_factor_bytes_per_unit": copy_bytes / out["WRITE_SIZE"][1]}, None
+        if not dec or not cal or not cpy:
+            return None, f"no {counter} rows for the decode or calibration kernels"
+        out[counter] = (median(dec), max(cal), {k: median(v) for k, v in fq.items() if v},
+                        max(cpy))
+    # Each calibration kernel moves 256 MiB in the counted direction: the
+    # factor converts counter units to bytes. The copy's factors are reported
+    # beside them (its reads can include line fills for its writes).
+    cal_bytes = 256 * 2 ** 20
+    ff = cal_bytes / out["FETCH_SIZE"][1]
+    wf = cal_bytes / out["WRITE_SIZE"][1]
+    fake = {name: {"fetch_bytes": out["FETCH_SIZE"][2][name] * ff,
+                   "write_bytes": out["WRITE_SIZE"][2][name] * wf}
+            for name in out["FETCH_SIZE"][2] if name in out["WRITE_SIZE"][2]}
+    return {"fetch_bytes": out["FETCH_SIZE"][0] * ff, "write_bytes": out["WRITE_SIZE"][0] * wf,
+            "fetch_factor_bytes_per_unit": ff, "write_factor_bytes_per_unit": wf,
+            "copy_fetch_factor_bytes_per_unit": cal_bytes / out["FETCH_SIZE"][3],
+            "copy_write_factor_bytes_per_unit": cal_bytes / out["WRITE_SIZE"][3],
+            "fake_quant": fake}, None
 
 
 def decode_kernel_label(w, value_dtype):
@@ -730,8 +759,13 @@ def main():
     if not args.no_pmc:
         traffic, err = pmc_traffic(args)
         if traffic is not None:
+            fake = traffic.pop("fake_quant")
             line["roofline"]["traffic"] = round(traffic["fetch_bytes"] + traffic["write_bytes"])
             line["roofline"]["traffic_detail"] = {k: round(v, 4) for k, v in traffic.items()}
+            for name, t in fake.items():
+                rec = line["fake_quant"][name]
+                rec["traffic"] = round(t["fetch_bytes"] + t["write_bytes"])
+                rec["traffic_vs_algorithmic"] = round(rec["traffic"] / rec["bytes"], 4)
         else:
             line["roofline"]["traffic_error"] = err
     if not args.no_cpu:
