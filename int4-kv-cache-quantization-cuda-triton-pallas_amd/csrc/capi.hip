@@ -81,11 +81,12 @@ bool use_mfma(int d) {
   return on && (d == 64 || d == 128);
 }
 
-// Eight heads per workgroup fit the registers at D=64, and at D=128 with
-// float32 values (254 VGPRs); float16 values at D=128 stop at four.
+// Up to eight heads per workgroup (at D=128: 248 VGPRs with float32 values,
+// 244 with float16, no spills).
 int pick_heads_per_wg_mfma(int d, int v_dtype, int hq_per_kv) {
-  const int fit = (d == 64 || v_dtype == FDI4_V_F32) ? 8 : 4;
-  const int cap = std::min(env_int("FDI4_DECODE_HEADS_PER_WG", 8), fit);
+  (void)d;
+  (void)v_dtype;
+  const int cap = std::min(env_int("FDI4_DECODE_HEADS_PER_WG", 8), 8);
   for (int hg : {8, 4, 2})
     if (hg <= cap && hq_per_kv % hg == 0) return hg;
   return 1;

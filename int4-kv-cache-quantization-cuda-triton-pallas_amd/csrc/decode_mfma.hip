@@ -47,16 +47,12 @@ struct MfmaGeo {
   static_assert(D == 64 || D == 128, "int8 MFMA decode: D = 64 or 128");
 };
 
-// Channel of MFMA slot j (0..15) within a lane's 16-channel piece: slots 0..7
-// are the low nibbles of the piece's bytes 0..7 (even channels), slots 8..15
-// the high nibbles (odd channels).
-__device__ __forceinline__ int piece_channel(int j) { return j < 8 ? 2 * j : 2 * (j - 8) + 1; }
-
-// Channel base of lane group g's piece kb.
-template <int D>
-__device__ __forceinline__ int piece_base(int g, int kb) {
-  return (D == 64) ? 16 * g : 32 * g + 16 * kb;
-}
+// Channel layout of the MFMA operands: lane group g (lanes 16g .. 16g+15)
+// holds the 16-channel piece kb of channels base = 16g (D = 64) or 32g + 16kb
+// (D = 128); slot j (byte j of the B operand) is channel base + 2j for
+// j < 8 (the low nibbles of the packed bytes) and base + 2(j-8) + 1 for
+// j >= 8 (the high nibbles), matching the A operand built from the packed
+// key words.
 
 template <int HG>
 struct HeadF {
@@ -87,6 +83,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
   __shared__ float acc_s[WAVES][HG][D];
   __shared__ double m_s[WAVES][HG];
   __shared__ float l_s[WAVES][HG];
+  // Per wave: the HG heads' B operands in MFMA lane layout [digit][block]
+  // [channel group][head][byte], their exponents and group constants.
+  __shared__ __attribute__((aligned(16))) uint8_t dig_s[WAVES][G::DIGITS][G::NB][4][HG][16];
+  __shared__ int hex_s[WAVES][HG];
+  __shared__ double hcg_s[WAVES][HG];
 
   const int cpp = (a.page_rows + 15) >> 4;
   const int T = seq_len_of(a, b);
@@ -143,54 +144,75 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
     }
   };
 
-  // Rebuild head n16's digits, exponent and group constant from the staged
-  // scale/zero-point block (channels of this lane's group).
+  // Rebuild the B operands (digits), exponents and group constants of the HG
+  // heads from the staged scale/zero-point block. The products are spread
+  // densely: lane l computes PPL channels of head l / LPH (every lane busy,
+  // whatever HG), and the digit bytes go through LDS into the MFMA lane
+  // layout (lane l's B operand: head l % 16, channel group l / 16), where a
+  // head lane reads them back as 16-byte words.
   auto rebuild = [&](const float* szw) {
+    constexpr int LPH = 64 / HG;        // lanes per head
+    constexpr int PPL = HG * D / 64;    // channels per lane
+    const int hh = lane / LPH;
+    const int d0 = (lane % LPH) * PPL;
+    const float* qh = q_s[hh];
     // Pass 1: the head's largest |q*s| (its exponent) and the group constant.
-    const float* qh = q_s[head_lane ? n16 : 0];
     double mx = 0.0, cgp = 0.0;
 #pragma unroll
-    for (int kb = 0; kb < G::NB; ++kb) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int d = piece_base<D>(grp, kb) + piece_channel(j);
-        const double qd = head_lane ? (double)qh[d] : 0.0;
-        const double sd = (double)szw[d];
-        mx = fmax(mx, fabs(qd * sd));
-        cgp = __builtin_fma(qd, (double)szw[D + d] * sd, cgp);
-      }
+    for (int i = 0; i < PPL; ++i) {
+      const int d = d0 + i;
+      const double qd = (double)qh[d];
+      const double sd = (double)szw[d];
+      mx = fmax(mx, fabs(qd * sd));
+      cgp = __builtin_fma(qd, (double)szw[D + d] * sd, cgp);
     }
-    mx = allreduce_max<16, 64>(mx);
-    cg = allreduce_sum<16, 64>(cgp);
+    mx = allreduce_max<1, LPH>(mx);
+    const double cgh = allreduce_sum<1, LPH>(cgp);
     int ex = 0;
     if (mx > 0.0) (void)frexp(mx, &ex);
-    e_head = ex;
-    // Pass 2: the products again (cheaper than keeping them), as digits.
+    // Pass 2: the products again (cheaper than keeping them), as digits at
+    // their B-operand byte: channel d is byte j of group g's block kb.
 #pragma unroll
-    for (int kb = 0; kb < G::NB; ++kb) {
-      unsigned dw[G::DIGITS][4];
+    for (int i = 0; i < PPL; ++i) {
+      const int d = d0 + i;
+      const double qsd = (double)qh[d] * (double)szw[d];
+      // v = rint(q*s * 2^(41 - e)), |v| <= 2^41; v = hi * 2^21 + lo, 0 <= lo < 2^21.
+      const double v = rint(ldexp(qsd, 41 - ex));
+      const double hi = floor(v * 0x1p-21);
+      const int hi_i = (int)hi;
+      const int lo_i = (int)(v - hi * 0x1p21);
+      const unsigned dig[G::DIGITS] = {
+          (unsigned)(hi_i >> 14) & 255u, (unsigned)(hi_i >> 7) & 127u, (unsigned)hi_i & 127u,
+          (unsigned)(lo_i >> 14) & 127u, (unsigned)(lo_i >> 7) & 127u, (unsigned)lo_i & 127u};
+      const int g = (D == 64) ? d / 16 : d / 32;
+      const int kb = (D == 64) ? 0 : (d / 16) & 1;
+      const int o = d & 15;
+      const int jb = (o & 1) ? 8 + (o >> 1) : (o >> 1);
+#pragma unroll
+      for (int dg = 0; dg < G::DIGITS; ++dg) dig_s[w][dg][kb][g][hh][jb] = (uint8_t)dig[dg];
+    }
+    if (lane % LPH == 0) {
+      hex_s[w][hh] = ex;
+      hcg_s[w][hh] = cgh;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (head_lane) {
 #pragma unroll
       for (int dg = 0; dg < G::DIGITS; ++dg)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) dw[dg][q] = 0u;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int d = piece_base<D>(grp, kb) + piece_channel(j);
-        const double qsd = (head_lane ? (double)qh[d] : 0.0) * (double)szw[d];
-        // v = rint(q*s * 2^(41 - e)), |v| <= 2^41; v = hi * 2^21 + lo, 0 <= lo < 2^21.
-        const double v = rint(ldexp(qsd, 41 - ex));
-        const double hi = floor(v * 0x1p-21);
-        const int hi_i = (int)hi;
-        const int lo_i = (int)(v - hi * 0x1p21);
-        const unsigned dig[G::DIGITS] = {
-            (unsigned)(hi_i >> 14) & 255u, (unsigned)(hi_i >> 7) & 127u, (unsigned)hi_i & 127u,
-            (unsigned)(lo_i >> 14) & 127u, (unsigned)(lo_i >> 7) & 127u, (unsigned)lo_i & 127u};
-#pragma unroll
-        for (int dg = 0; dg < G::DIGITS; ++dg) dw[dg][j / 4] |= dig[dg] << (8 * (j % 4));
-      }
+        for (int kb = 0; kb < G::NB; ++kb)
+          bq[dg][kb] = *reinterpret_cast<const v4i*>(&dig_s[w][dg][kb][grp][n16][0]);
+      e_head = hex_s[w][n16];
+      cg = hcg_s[w][n16];
+    } else {
 #pragma unroll
       for (int dg = 0; dg < G::DIGITS; ++dg)
-        bq[dg][kb] = v4i{(int)dw[dg][0], (int)dw[dg][1], (int)dw[dg][2], (int)dw[dg][3]};
+#pragma unroll
+        for (int kb = 0; kb < G::NB; ++kb) bq[dg][kb] = v4i{0, 0, 0, 0};
+      e_head = 0;
+      cg = 0.0;
     }
   };
 
@@ -386,10 +408,8 @@ hipError_t launch_decode_mfma(const DecodeArgs& a, int D, int v_dtype, int batch
   FDI4_MF(64, kVF32, WW, HH) FDI4_MF(128, kVF32, WW, HH)                                  \
   FDI4_MF(64, kVF16, WW, HH) FDI4_MF(128, kVF16, WW, HH)
   FDI4_MF_H(4, 2) FDI4_MF_H(8, 2) FDI4_MF_H(4, 4) FDI4_MF_H(8, 4)
-  // Eight heads per workgroup at D=64, and at D=128 with float32 values (with
-  // float16 values the registers run out).
-  FDI4_MF(64, kVF32, 4, 8) FDI4_MF(64, kVF32, 8, 8) FDI4_MF(64, kVF16, 4, 8)
-  FDI4_MF(64, kVF16, 8, 8) FDI4_MF(128, kVF32, 4, 8) FDI4_MF(128, kVF32, 8, 8)
+  // Eight heads per workgroup.
+  FDI4_MF_H(4, 8) FDI4_MF_H(8, 8)
 #undef FDI4_MF_H
 #undef FDI4_MF
   return hipErrorInvalidValue;
