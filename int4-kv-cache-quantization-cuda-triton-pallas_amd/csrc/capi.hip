@@ -138,6 +138,8 @@ int check_cache(const fdi4_paged_cache* c, bool need_values) {
   if (!aligned(c->k_pages, kbl) || c->k_page_stride % kbl || c->k_head_stride % kbl ||
       c->k_row_stride % kbl || c->k_row_stride < c->head_dim / 2)
     return hipErrorInvalidValue;
+  // The kernels address the rows of a 16-row chunk with 32-bit byte offsets.
+  if ((int64_t)c->k_row_stride * 16 + c->head_dim > INT32_MAX) return hipErrorInvalidValue;
   if (!aligned(c->k_scale, 16) || !aligned(c->k_zp, 16) || c->s_batch_stride % 4 ||
       c->s_head_stride % 4 || c->s_group_stride % 4 || c->s_page_stride % 4)
     return hipErrorInvalidValue;
@@ -148,6 +150,8 @@ int check_cache(const fdi4_paged_cache* c, bool need_values) {
     if (!aligned(c->v_pages, 16) || (c->v_page_stride * veb) % 16 ||
         (c->v_head_stride * veb) % 16 || (c->v_row_stride * veb) % 16 ||
         c->v_row_stride < c->head_dim)
+      return hipErrorInvalidValue;
+    if ((c->v_row_stride * veb) * 16 + (int64_t)c->head_dim * veb > INT32_MAX)
       return hipErrorInvalidValue;
   }
   return hipSuccess;

@@ -104,10 +104,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
 
   const float* sbase = a.k_scale + (int64_t)b * a.s_b + (int64_t)hk * a.s_h;
   const float* zbase = a.k_zp + (int64_t)b * a.s_b + (int64_t)hk * a.s_h;
-  const uint8_t* kbase0 = a.k_pages + (int64_t)hk * a.k_head + kq * G::KBL;
-  const uint8_t* vbase0 = reinterpret_cast<const uint8_t*>(a.v_pages) +
-                          (int64_t)hk * a.v_head * G::VEB + vcol * 16;
-  const int64_t vrow_b = a.v_row * G::VEB;
+  // Page bases are wave-uniform (scalar registers); each lane adds a 32-bit
+  // byte offset (its channel slice and row), so the loads take the
+  // scalar-base + vector-offset form with no 64-bit address arithmetic per
+  // lane (row strides are checked on the host: 16 rows fit in 31 bits).
+  const uint8_t* kbase_h = a.k_pages + (int64_t)hk * a.k_head;
+  const uint8_t* vbase_h = reinterpret_cast<const uint8_t*>(a.v_pages) +
+                           (int64_t)hk * a.v_head * G::VEB;
+  const unsigned k_lane = kq * G::KBL, v_lane = vcol * 16;
+  const unsigned krow_b = (unsigned)a.k_row, vrow_b = (unsigned)(a.v_row * G::VEB);
 
   // Scale/zero-point block of one group: items 0..D/4-1 are scale[4e..4e+3],
   // items D/4..D/2-1 are zp. Lanes past the block reload an in-range item.
@@ -122,17 +127,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   };
 
   auto load_chunk = [&](const ChunkMeta& m, KVec<G::KW>* kr, U32x4* vr) {
-    const uint8_t* kb = kbase0 + m.phys * a.k_page + (int64_t)m.r0 * a.k_row;
+    const uint8_t* kb = kbase_h + m.phys * a.k_page + (int64_t)m.r0 * a.k_row;
 #pragma unroll
     for (int i = 0; i < G::KLD; ++i) {
       const int t = max(min(i * G::TPW + ktok, m.nval - 1), 0);
-      kr[i] = load_k<G::KW>(kb + (int64_t)t * a.k_row);
+      kr[i] = load_k<G::KW>(kb + (k_lane + (unsigned)t * krow_b));
     }
-    const uint8_t* vb = vbase0 + (m.phys * a.v_page + (int64_t)m.r0 * a.v_row) * G::VEB;
+    const uint8_t* vb = vbase_h + (m.phys * a.v_page + (int64_t)m.r0 * a.v_row) * G::VEB;
 #pragma unroll
     for (int i = 0; i < G::VLD; ++i) {
       const int r = max(min(i * G::RPL + vrow, m.nval - 1), 0);
-      vr[i] = ld16_stream(vb + (int64_t)r * vrow_b);
+      vr[i] = ld16_stream(vb + (v_lane + (unsigned)r * vrow_b));
     }
   };
 
