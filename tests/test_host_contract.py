@@ -2,6 +2,7 @@
 backend honesty, the storage helpers, the workload byte model, and the C-ABI
 library's exported surface."""
 
+import ctypes
 import os
 import re
 
@@ -252,3 +253,17 @@ class TestCABI:
         assert lib.fdi4_merge_splits(None, None, 1, 1, 128, 1, None, 0, 0, None) == bad
         assert lib.fdi4_flash_decode_int4_ws(None, None, None, None, None, None, 1, 1, 300, 1, 1,
                                              None, None, 0, None) == bad
+        # Row strides whose 16-row chunk does not fit in 31 bits of byte
+        # offset (the kernels address a chunk's rows with 32-bit offsets).
+        big = capi.PagedCache(head_dim=128, page_rows=16, num_kv_heads=1, pages_per_group=8,
+                              max_pages=8, num_pages=8, k_pages=256, k_scale=256, k_zp=256,
+                              k_page_stride=1 << 30, k_row_stride=1 << 27,
+                              v_pages=256, v_dtype=capi.V_F32, v_page_stride=1 << 12,
+                              v_row_stride=128, s_group_stride=128, seq_lens=256)
+        q = ctypes.c_void_p(256)
+        assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
+                                     None, 0, None) == bad
+        big.k_row_stride = 64
+        big.v_row_stride = 1 << 25
+        assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
+                                     None, 0, None) == bad
