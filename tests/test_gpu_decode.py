@@ -307,7 +307,10 @@ class TestGroupedQueryHeads:
         (256, 2, "float16", [129, 700], 0),
         (128, 6, "float32", [400, 77], 0),   # groups of 2
         (128, 3, "float32", [400, 77], 0),   # per-head kernel
-        (128, 8, "float32", [1200, 5], 0),   # groups of 4 at D=128
+        (128, 8, "float32", [1200, 5], 0),   # eight heads per workgroup at D=128
+        (128, 8, "float16", [1200, 5, 0], 0),
+        (128, 16, "float16", [300, 2000], 0),  # two workgroups of 8 per kv-head
+        (64, 8, "float16", [700, 33], 3),
     ])
     def test_matches_oracle(self, D, rep, vdtype, lens, splits):
         import torch
@@ -329,15 +332,18 @@ class TestGroupedQueryHeads:
         empty = np.asarray(lens) == 0
         assert np.all(out[empty] == 0.0)
 
-    @pytest.mark.parametrize("D,rep", [(128, 4), (64, 8), (128, 2), (128, 8)])
-    def test_matrix_core_equals_vector_kernel(self, monkeypatch, D, rep):
+    @pytest.mark.parametrize("D,rep,vdtype", [(128, 4, None), (64, 8, None), (128, 2, None),
+                                              (128, 8, None), (128, 8, "float16"),
+                                              (64, 4, "float16")])
+    def test_matrix_core_equals_vector_kernel(self, monkeypatch, D, rep, vdtype):
         """The int8 matrix-core kernel's logits are exact up to the 41-bit
         rounding of q*s; it agrees with the vector grouped kernel (fp64
         products) to float32 rounding."""
         import torch
         from flash_decode_int4.workloads import make_workload
         w = make_workload(batch=2, heads=2, head_dim=D, seq_lens=[1500, 333], seed=D + rep)
-        q_t, kp, v_t, s, z, pt, sl = _paged_device(w)
+        q_t, kp, v_t, s, z, pt, sl = _paged_device(
+            w, value_dtype=torch.float16 if vdtype else None)
         q = torch.randn(2, 2 * rep, D, device="cuda", generator=torch.Generator("cuda").manual_seed(7))
         mfma = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=2)
         monkeypatch.setenv("FDI4_DECODE_MFMA", "0")
