@@ -24,6 +24,9 @@ reference_config times the drop-in API (prepare_flash_decode_hip().run()) on
 the reference's own benchmark semantics, beside the reference's published
 CUDA time for it on other hardware (context, not vs_baseline).
 
+other_paths times the decode with fp16 value pages at the anchor shape and with
+grouped-query heads (B8, 8 kv-heads, 32 q-heads, 8192 tokens).
+
 fake_quant times the quality-study kernel (INT4 quantize-dequantize of a key
 tensor in blocks) on a Llama-2-7B-sized perplexity window and on the decode
 workload's keys, beside the same computation as eager torch operations.
@@ -408,6 +411,35 @@ def time_fake_quant(steps, warmup):
     return out
 
 
+def time_other_paths(args):
+    """Decode timings of the paths beside the headline one, on their own
+    workloads (inputs rotated past the Infinity Cache as for the headline):
+    fp16 value pages at the anchor shape, and grouped-query heads (B8, 8
+    kv-heads, 32 q-heads, 8192 tokens). Skipped when the headline workload is
+    already one of them."""
+    import torch
+    from flash_decode_int4 import workloads
+    out = {}
+    cases = (("fp16_values", "anchor", "float16"), ("grouped_query", "gqa", "float32"))
+    for key, name, vdt in cases:
+        if name == args.workload and vdt == args.value_dtype:
+            continue
+        sets, nbytes = build_sets(name, vdt)
+        r = time_decode(sets, 0, args.steps, args.warmup)
+        w = sets[0]["w"]
+        out[key] = {
+            "workload": f"{name}: B{w['batch']} Hkv{w['heads']} Hq{w['q_heads']} D{w['head_dim']} "
+                        f"T{int(max(w['seq_lens']))}, {vdt} values",
+            "kernel": decode_kernel_label(w, vdt), "num_splits": r["splits"],
+            "bytes": nbytes, "decode_us": round(r["step_us"], 3),
+            "gbs": round(nbytes / (r["step_us"] * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "finite": bool(torch.isfinite(r["last_out"]).all())}
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
 def median(x):
     s = sorted(x)
     n = len(s)
@@ -686,6 +718,7 @@ def main():
     probe = hbm_probes()
     refcfg = time_reference_config(args.steps, args.warmup)
     fq = time_fake_quant(args.steps, args.warmup)
+    other = time_other_paths(args)
 
     # No shape specialization (the reference bench re-runs at seq_len + 1): every
     # length + 1, so pages end one row into a fresh page and groups one row into
@@ -739,6 +772,7 @@ def main():
         "hbm_probe": probe,
         "reference_config": refcfg,
         "fake_quant": fq,
+        "other_paths": other,
         "checks": {
             "split_invariance_max_abs": gate,
             "seq_len_plus_1": {
