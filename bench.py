@@ -25,7 +25,9 @@ the reference's own benchmark semantics, beside the reference's published
 CUDA time for it on other hardware (context, not vs_baseline).
 
 other_paths times the decode with fp16 value pages at the anchor shape and with
-grouped-query heads (B8, 8 kv-heads, 32 q-heads, 8192 tokens).
+grouped-query heads (B8, 8 kv-heads, 32 q-heads, 8192 tokens), and the serving
+loop's step (append + length advance + decode) on the sequence cache, issued
+eagerly and as a replayed HIP graph.
 
 fake_quant times the quality-study kernel (INT4 quantize-dequantize of a key
 tensor in blocks) on a Llama-2-7B-sized perplexity window and on the decode
@@ -440,6 +442,56 @@ def time_other_paths(args):
     return out
 
 
+def time_decode_step(args, B=8, H=32, D=128, T=2048):
+    """The serving loop's step on the sequence cache (fp32 values, B sequences
+    of H heads from T tokens): append one token per (sequence, kv-head),
+    advance the lengths, decode -- issued eagerly from Python, and as one
+    captured HIP graph replayed (the same kernels without the host's per-call
+    work). Each step adds a token, so the cache grows by one row per step."""
+    import torch
+    from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
+    n = args.warmup + 2 * args.steps + 2
+    cache = INT4PagedSequenceCache(num_pages=B * ((T + n) // 16 + 2), num_kv_heads=H, head_dim=D,
+                                   max_seqs=B, max_seq_len=T + n)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    k = torch.randn(B, H, T, D, device="cuda", generator=g)
+    cache.prefill(k, torch.randn_like(k), [T] * B)
+    del k
+    cache.reserve(B, n)
+    kn = torch.randn(B, H, D, device="cuda", generator=g)
+    vn = torch.randn(B, H, D, device="cuda", generator=g)
+    q = torch.randn(B, H, D, device="cuda", generator=g)
+
+    def timed(fn, steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    for _ in range(args.warmup):
+        cache.step(kn, vn, q)
+    eager = timed(lambda: cache.step(kn, vn, q), args.steps)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = cache.step(kn, vn, q)
+    replay = timed(graph.replay, args.steps)
+    ok = bool(torch.isfinite(out).all())
+    cache.sync_lengths()
+    res = {"workload": f"B{B} H{H} D{D} from {T} tokens, fp32 values: append + length "
+                       "advance + decode per step",
+           "eager_us": round(eager, 3), "graph_replay_us": round(replay, 3), "finite": ok,
+           "final_length": int(cache.lengths()[0])}
+    del cache, graph
+    torch.cuda.empty_cache()
+    return res
+
+
 def median(x):
     s = sorted(x)
     n = len(s)
@@ -719,6 +771,8 @@ def main():
     refcfg = time_reference_config(args.steps, args.warmup)
     fq = time_fake_quant(args.steps, args.warmup)
     other = time_other_paths(args)
+    other["decode_step"] = time_decode_step(args)
+    other["decode_step_small"] = time_decode_step(args, B=1, H=8, D=128, T=1024)
 
     # No shape specialization (the reference bench re-runs at seq_len + 1): every
     # length + 1, so pages end one row into a fresh page and groups one row into

@@ -289,6 +289,36 @@ class INT4PagedSequenceCache:
         self.seq_lens[:B] += 1
         self._lens[:B] += 1
 
+    # ---- device-only decode steps (graph capture) ----------------------------
+
+    def reserve(self, batch: int, n_tokens: int) -> None:
+        """Map the pages sequences 0..batch-1 need to grow by n_tokens, so that
+        step() does no host work until they have."""
+        updates = []
+        for b in range(batch):
+            self._grow(b, int(self._lens[b]) + n_tokens, updates)
+        self._apply(updates)
+
+    def step(self, k_new, v_new, query, num_splits: int = 0):
+        """One decode step on the device alone: append (k_new, v_new) [B,
+        kv_heads, D] at each sequence's length, advance the lengths on the
+        device, attend with query [B, Hq, D]; returns float32 [B, Hq, D].
+        No host bookkeeping happens, so the call can be captured in a HIP
+        graph and replayed: the pages must already be mapped (reserve), and
+        lengths() reflects the steps only after sync_lengths()."""
+        B = k_new.shape[0]
+        if B > self.max_seqs or tuple(k_new.shape) != (B, self.num_kv_heads, self.head_dim):
+            raise ValueError("k_new must be [batch <= max_seqs, kv_heads, head_dim]")
+        load_binding().append_paged(k_new, v_new, self.k_stage[:B], self.k_pages,
+                                    self.v_pages, self.k_scale[:B], self.k_zp[:B],
+                                    self.page_table[:B], self.seq_lens[:B], self.group_rows)
+        self.seq_lens[:B] += 1
+        return self.decode(query, num_splits)
+
+    def sync_lengths(self) -> None:
+        """Refresh the host copy of the lengths from the device (after step())."""
+        self._lens[:] = self.seq_lens.cpu().numpy()
+
     # ---- reads -------------------------------------------------------------
 
     def decode(self, query, num_splits: int = 0):

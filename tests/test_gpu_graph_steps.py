@@ -1,0 +1,94 @@
+"""Decode steps captured in a HIP graph.
+
+A serving loop appends one token per sequence and attends, every step. The
+sequence cache's step() does both on the device alone (append kernel, length
+advance, decode), so one step can be captured and replayed. Two identical
+caches are driven side by side, one eagerly and one by graph replays with new
+inputs copied in between; every replay's output and the final pages, scales,
+values and lengths must equal the eager ones bit for bit, and the eager path
+must match the oracle.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import paged_decode_f64, paged_decode_ref, quantize_groups_ref, pack_int4
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _cache(value_dtype):
+    from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
+    return INT4PagedSequenceCache(num_pages=256, num_kv_heads=4, head_dim=128, max_seqs=3,
+                                  max_seq_len=1024, value_dtype=value_dtype)
+
+
+@pytest.mark.parametrize("value_dtype,q_heads,steps", [("float32", 4, 6), ("float16", 16, 5)])
+def test_graph_replayed_steps_equal_eager_steps(value_dtype, q_heads, steps):
+    import torch
+    vdt = getattr(torch, value_dtype)
+    B, H, D, T0 = 3, 4, 128, 400
+    lens0 = [100, 127, 300]                      # 127: the first step closes a group
+    g = torch.Generator(device="cuda").manual_seed(5)
+    k = torch.randn(B, H, T0, D, device="cuda", generator=g)
+    v = torch.randn(B, H, T0, D, device="cuda", generator=g).to(vdt)
+    eager, graphed = _cache(value_dtype), _cache(value_dtype)
+    for c in (eager, graphed):
+        c.prefill(k, v, lens0)
+        c.reserve(B, steps + 1)
+    k_in = [torch.randn(B, H, D, device="cuda", generator=g) for _ in range(steps + 1)]
+    v_in = [torch.randn(B, H, D, device="cuda", generator=g).to(vdt) for _ in range(steps + 1)]
+    q_in = [torch.randn(B, q_heads, D, device="cuda", generator=g) for _ in range(steps + 1)]
+
+    # Step 0 eagerly on both (warm-up outside the capture), then capture step 1.
+    eager_out = [eager.step(k_in[0], v_in[0], q_in[0])]
+    graphed.step(k_in[0], v_in[0], q_in[0])
+    k_s, v_s, q_s = k_in[1].clone(), v_in[1].clone(), q_in[1].clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_s = graphed.step(k_s, v_s, q_s)
+    # Capturing recorded the step without running it.
+    for i in range(1, steps + 1):
+        eager_out.append(eager.step(k_in[i], v_in[i], q_in[i]))
+        torch.cuda.synchronize()
+        k_s.copy_(k_in[i])
+        v_s.copy_(v_in[i])
+        q_s.copy_(q_in[i])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_s, eager_out[i]), i
+    for name in ("k_pages", "v_pages", "k_scale", "k_zp", "seq_lens", "k_stage"):
+        assert torch.equal(getattr(graphed, name), getattr(eager, name)), name
+    graphed.sync_lengths()
+    assert list(graphed.lengths()[:B]) == [n + steps + 1 for n in lens0]
+
+    # The eager path against the oracle after the last step.
+    n = [l0 + steps + 1 for l0 in lens0]
+    kk = torch.zeros(B, H, max(n), D, device="cuda")
+    vv = torch.zeros(B, H, max(n), D, device="cuda")
+    for b in range(B):
+        kk[b, :, :lens0[b]] = k[b, :, :lens0[b]]
+        vv[b, :, :lens0[b]] = v[b, :, :lens0[b]].float()
+        for i in range(steps + 1):
+            kk[b, :, lens0[b] + i] = k_in[i][b]
+            vv[b, :, lens0[b] + i] = v_in[i][b].float()
+    qr, sr, zr = quantize_groups_ref(kk.cpu().numpy(), np.array(n))
+    sc = eager.k_scale[:B].cpu().numpy()
+    for b in range(B):
+        ng = (n[b] + 127) // 128
+        np.testing.assert_array_equal(sc[b, :, :ng], sr[b, :, :ng])
+    table = eager.page_table[:B].cpu().numpy()
+    kp = eager.k_pages.cpu().numpy()
+    vp = eager.v_pages.float().cpu().numpy()
+    for b in range(B):
+        npg = (n[b] + 15) // 16
+        got = kp[table[b, :npg]].transpose(1, 0, 2, 3).reshape(H, npg * 16, D // 2)[:, :n[b]]
+        np.testing.assert_array_equal(got, pack_int4(qr[b, :, :n[b]]))
+    args = (q_in[steps].cpu().numpy(), kp, vp, sc, eager.k_zp[:B].cpu().numpy(), table,
+            np.array(n, np.int32))
+    o32, o64 = paged_decode_ref(*args), paged_decode_f64(*args)
+    got = eager_out[steps].cpu().numpy()
+    assert np.abs(got - o32).max() <= max(TOL, 1.25 * np.abs(o32 - o64).max())
