@@ -39,6 +39,7 @@
 // correction (Markstein), which is the correctly rounded IEEE quotient for
 // 0 <= x - mn <= span, scale >= 1e-8 / 15.
 
+#include <limits.h>
 #include <stdlib.h>
 
 #include "../../include/fdi4.h"
@@ -288,7 +289,9 @@ hipError_t launch_fake_quant(const FakeQuantArgs& args, int key_dtype, int round
   // against 15.2 and 12.2 us). FDI4_FAKE_QUANT_SPLIT overrides (tuning).
   const int row_bytes = a.head_dim * esz;
   int split = env_int("FDI4_FAKE_QUANT_SPLIT", row_bytes >= 128 ? row_bytes / 128 : 1);
-  while (split > 1 && (a.head_dim % split || (a.head_dim / split * esz) % 16)) --split;
+  while (split > 1 && (a.head_dim % split || (a.head_dim / split * esz) % 16 ||
+                       nblk * split > INT32_MAX))
+    --split;
   a.nsplit = max(split, 1);
   a.cw = a.head_dim / a.nsplit;
   a.vpr = a.cw * esz / 16;
