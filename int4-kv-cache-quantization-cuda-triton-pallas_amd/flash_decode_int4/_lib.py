@@ -23,10 +23,11 @@ def load_binding():
         return _binding
     if _binding_error is not None:
         raise RuntimeError(_binding_error)
+    # A missing build is not remembered: a build in the same process (the
+    # package is imported before it compiles) must be able to load it after.
     if not os.path.exists(os.path.join(PKG_DIR, "_C.so")) or not os.path.exists(LIB_PATH):
-        _binding_error = ("the HIP extension is not built (missing _C.so / libfdi4.so in "
-                          f"{PKG_DIR}); run `python -m flash_decode_int4._build`")
-        raise RuntimeError(_binding_error)
+        raise RuntimeError("the HIP extension is not built (missing _C.so / libfdi4.so in "
+                           f"{PKG_DIR}); run `python -m flash_decode_int4._build`")
     try:
         import torch  # noqa: F401  (the binding links against torch's libraries)
         _binding = importlib.import_module(__package__ + "._C")
