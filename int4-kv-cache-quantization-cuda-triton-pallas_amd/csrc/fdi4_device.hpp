@@ -104,6 +104,20 @@ __device__ __forceinline__ float allreduce_max_f(float x) {
   return x;
 }
 
+// ---- workgroup -> work item mapping across the XCDs ----------------------------
+
+// The dispatcher hands workgroup L of a one-dimensional grid of N to XCD
+// L % 8. This returns the work item W that workgroup L processes such that
+// the items are dealt to the XCDs in runs of C consecutive items (XCD x
+// processes runs x, x + 8, x + 16, ... in order); the tail of N that does not
+// fill a whole round of 8 runs keeps W = L. It is a bijection of [0, N).
+__device__ __forceinline__ unsigned xcd_run_item(unsigned L, unsigned N, unsigned C) {
+  const unsigned full = N / (8 * C) * (8 * C);
+  if (L >= full) return L;
+  const unsigned xcd = L % 8, j = L / 8;
+  return ((j / C) * 8 + xcd) * C + j % C;
+}
+
 // ---- 16-byte global access ----------------------------------------------------
 
 struct alignas(16) U32x4 {

@@ -19,7 +19,8 @@
 //       (reference csrc/flash_decode_int4.cu:27-83), split over row tiles so
 //       that any row count fills the chip; unpacked or nibble-packed output.
 //   quantize_paged_kernel<D, GROUP>
-//       one workgroup per (group, kv-head, sequence): 16-byte token-major
+//       one workgroup per (group, kv-head, sequence), dealt to the XCDs in
+//       runs of consecutive groups of a (sequence, kv-head): 16-byte token-major
 //       non-temporal loads held in registers, wave64 min/max reduction,
 //       quantize from registers, nibble pack, and 16-byte non-temporal stores
 //       of whole page rows through the page table.
@@ -290,12 +291,24 @@ __device__ __forceinline__ void quantize_group(const QuantPagedArgs& a, int b, i
   }
 }
 
+// Scale groups per XCD run: the groups of one (sequence, kv-head) are
+// consecutive work items, so a run of 16 keeps up to 16 x 64 KiB (D = 128) of
+// contiguous key rows on one XCD. Measured on MI355X against the plain
+// (group, head, sequence) grid: anchor keys 56.8 -> 55.8 us, Llama-sized keys
+// 934 -> 895 us, bit-identical output.
+constexpr unsigned kQRun = 16;
+
 // One workgroup quantizes the rows [g*GROUP, min((g+1)*GROUP, T_b)) of one
-// (sequence b, kv-head h) of the key tensor.
+// (sequence b, kv-head h) of the key tensor. One-dimensional grid over the
+// work items g + ngroups * (h + heads * b), dealt to the XCDs in runs.
 template <int D, int GROUP>
-__global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArgs a) {
+__global__ __launch_bounds__(kQThreads) void quantize_paged_kernel(QuantPagedArgs a, int ngroups,
+                                                                   int heads) {
   using G = QGeo<D, GROUP>;
-  const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const unsigned wi = xcd_run_item(blockIdx.x, gridDim.x, kQRun);
+  const int g = (int)(wi % (unsigned)ngroups);
+  const int h = (int)(wi / (unsigned)ngroups % (unsigned)heads);
+  const int b = (int)(wi / ((unsigned)ngroups * (unsigned)heads));
   const int T = min(a.seq_lens[b], a.max_tokens);
   const int r0 = g * GROUP;
   if (r0 >= T) return;
@@ -360,11 +373,14 @@ hipError_t launch_quantize_paged(const QuantPagedArgs& a, int D, int group, int 
                                  int max_tokens, hipStream_t st) {
   const int ngroups = (max_tokens + group - 1) / group;
   if (ngroups == 0 || batch == 0 || heads == 0) return hipSuccess;
-  dim3 grid(ngroups, heads, batch);
-#define FDI4_QP(DD, GG)                                                                  \
-  if (D == DD && group == GG) {                                                          \
-    hipLaunchKernelGGL((quantize_paged_kernel<DD, GG>), grid, dim3(kQThreads), 0, st, a); \
-    return hipGetLastError();                                                            \
+  const int64_t items = (int64_t)ngroups * heads * batch;
+  if (items > INT32_MAX) return hipErrorInvalidValue;
+  dim3 grid((unsigned)items);
+#define FDI4_QP(DD, GG)                                                             \
+  if (D == DD && group == GG) {                                                     \
+    hipLaunchKernelGGL((quantize_paged_kernel<DD, GG>), grid, dim3(kQThreads), 0, st, a, \
+                       ngroups, heads);                                             \
+    return hipGetLastError();                                                       \
   }
   FDI4_QP(64, 64) FDI4_QP(64, 128) FDI4_QP(64, 256)
   FDI4_QP(128, 64) FDI4_QP(128, 128) FDI4_QP(128, 256)
