@@ -24,6 +24,11 @@ reference_config times the drop-in API (prepare_flash_decode_hip().run()) on
 the reference's own benchmark semantics, beside the reference's published
 CUDA time for it on other hardware (context, not vs_baseline).
 
+reference_quantizer times the drop-in quantize_int4 (one scale group over all
+rows of a [rows, 128] array, unpacked bins) at the two row counts the
+reference publishes CUDA times for, beside those times; the CPU leg checks its
+bins, scales and zero-points bit for bit against the oracle.
+
 other_paths times the decode with fp16 value pages at the anchor shape and with
 grouped-query heads (B8, 8 kv-heads, 32 q-heads, 8192 tokens), and the serving
 loop's step (append + length advance + decode) on the sequence cache, issued
@@ -165,6 +170,65 @@ def time_reference_config(steps, warmup):
             "reference_cuda_h100_us": 400.0,
             "note": "the reference's published CUDA time for this configuration on an "
                     "NVIDIA H100 (its README and results JSON); other hardware, context only"}
+
+
+def time_reference_quantizer(steps, warmup):
+    """The reference's own quantizer benchmark semantics through the drop-in
+    API: ops.quantize_int4 of one [rows, 128] float32 array, one scale group
+    over all rows, one unpacked INT4 value per output byte (reference
+    benchmarks/bench_three_backend.py:141-159, src/ops.py:111-161), at the
+    two row counts the reference publishes CUDA times for. run() of
+    prepare_quantize_int4_hip is timed over input sets rotated past twice the
+    Infinity Cache. Bytes: the input read once, the unpacked bins and the
+    scale/zero-point rows written. Returns the record and, per row count, the
+    first set's input and outputs on the host for the CPU leg's bit-for-bit
+    check against the oracle."""
+    import torch
+    from flash_decode_int4 import ops
+    out, host = {}, {}
+    published_us = {2048: 15.4, 32768: 149.6}
+    for rows, ref_us in published_us.items():
+        C = 128
+        in_bytes = rows * C * 4
+        n_sets = max(2, math.ceil(2 * INFINITY_CACHE / in_bytes) + 1)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(4321)
+        sets = [torch.randn(rows, C, generator=g, device="cuda") for _ in range(n_sets)]
+        calls = [ops.prepare_quantize_int4_hip(k) for k in sets]
+        host[f"rows_{rows}x{C}"] = (sets[0].cpu().numpy(), calls[0]())
+        for i in range(warmup):
+            calls[i % n_sets].run()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(steps):
+            calls[i % n_sets].run()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        nbytes = in_bytes + rows * C + 2 * C * 4
+        out[f"rows_{rows}x{C}"] = {
+            "us": round(us, 3), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "input_sets": n_sets, "reference_cuda_h100_us": ref_us}
+        del sets, calls
+        torch.cuda.empty_cache()
+    out["note"] = ("reference's published CUDA quantizer times on an NVIDIA H100 "
+                   "(results/three_backend_quantize_h100.json); other hardware, context only")
+    return out, host
+
+
+def cpu_check_reference_quantizer(host):
+    """CPU leg: the NumPy oracle on the first input set of each row count of
+    time_reference_quantizer, compared bit for bit with the device's bins,
+    scales and zero-points."""
+    import numpy as np
+    from oracle import quantize_int4_ref
+    res = {}
+    for name, (kv, (q, s, z)) in host.items():
+        rq, rs, rz = quantize_int4_ref(kv)
+        res[name] = bool(np.array_equal(q, rq) and np.array_equal(s, rs)
+                         and np.array_equal(z, rz))
+    return res
 
 
 def blocked_median_us(fn, n, block=10):
@@ -769,6 +833,7 @@ def main():
     app = time_append(w0, args.value_dtype, args.steps, args.warmup)
     probe = hbm_probes()
     refcfg = time_reference_config(args.steps, args.warmup)
+    refq, refq_host = time_reference_quantizer(args.steps, args.warmup)
     fq = time_fake_quant(args.steps, args.warmup)
     other = time_other_paths(args)
     other["decode_step"] = time_decode_step(args)
@@ -825,6 +890,7 @@ def main():
         "append_us": app,
         "hbm_probe": probe,
         "reference_config": refcfg,
+        "reference_quantizer": refq,
         "fake_quant": fq,
         "other_paths": other,
         "checks": {
@@ -861,6 +927,8 @@ def main():
         base, parity = cpu_baseline(st, res["last_out"], args.cpu_runs, vbytes)
         line["cpu_baseline"] = base
         line["parity"] = parity
+        for name, exact in cpu_check_reference_quantizer(refq_host).items():
+            line["reference_quantizer"][name]["bit_exact_vs_oracle"] = exact
     print(json.dumps(line), flush=True)
 
 

@@ -148,6 +148,284 @@ __global__ __launch_bounds__(kRowsThreads) void rows_quantize_kernel(
   }
 }
 
+// ---- 2-D contract, 16-byte path (C % 4 == 0, 16-byte aligned rows) -------------
+//
+// A row's channels are cut into slices of 32 (128 bytes, one cache line);
+// eight lanes cover a slice of one row with one 16-byte load each, so a wave
+// reads 8 rows of a slice and every load instruction is independent of the
+// others (the scalar kernels above make one dependent 4-byte load per row and
+// are latency-bound). Lanes of an idle slice tail (C not a multiple of 32)
+// load the last full 4-channel group and store nothing.
+
+constexpr int kSliceCh = 32;
+
+struct RowsVecArgs {
+  const float* kv;
+  int64_t rows, stride;                  // elements
+  int C;
+  uint8_t* q;
+  int64_t q_stride;                      // bytes
+  int packed;                            // nibble pairs, else one bin per byte
+  int q_word;                            // q and q_stride allow 4-byte (2-byte packed) stores
+  float* scale;
+  float* zp;
+};
+
+// Extremes of this thread's NI float4 into mn/mx (4 channels each).
+template <int NI>
+__device__ __forceinline__ void minmax4(const float4* x, float* mn, float* mx) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    mn[k] = INFINITY;
+    mx[k] = -INFINITY;
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    mn[0] = fminf(mn[0], x[i].x); mx[0] = fmaxf(mx[0], x[i].x);
+    mn[1] = fminf(mn[1], x[i].y); mx[1] = fmaxf(mx[1], x[i].y);
+    mn[2] = fminf(mn[2], x[i].z); mx[2] = fmaxf(mx[2], x[i].z);
+    mn[3] = fminf(mn[3], x[i].w); mx[3] = fmaxf(mx[3], x[i].w);
+  }
+}
+
+// Bins of one row's 4 channels c0..c0+3, stored unpacked (4 bytes) or packed
+// (2 bytes) at row r.
+__device__ __forceinline__ void store_bins4(const RowsVecArgs& a, int64_t r, int c0, float4 x,
+                                            const float* mn, const float* sc, const float* rc) {
+  const unsigned n0 = (unsigned)quant_bin_rc(x.x, mn[0], sc[0], rc[0]);
+  const unsigned n1 = (unsigned)quant_bin_rc(x.y, mn[1], sc[1], rc[1]);
+  const unsigned n2 = (unsigned)quant_bin_rc(x.z, mn[2], sc[2], rc[2]);
+  const unsigned n3 = (unsigned)quant_bin_rc(x.w, mn[3], sc[3], rc[3]);
+  uint8_t* row = a.q + r * a.q_stride;
+  if (!a.packed) {
+    if (a.q_word) {
+      *reinterpret_cast<unsigned*>(row + c0) = n0 | (n1 << 8) | (n2 << 16) | (n3 << 24);
+    } else {
+      row[c0] = (uint8_t)n0; row[c0 + 1] = (uint8_t)n1;
+      row[c0 + 2] = (uint8_t)n2; row[c0 + 3] = (uint8_t)n3;
+    }
+  } else {
+    const unsigned lo = n0 | (n1 << 4), hi = n2 | (n3 << 4);
+    if (a.q_word) {
+      *reinterpret_cast<uint16_t*>(row + c0 / 2) = (uint16_t)(lo | (hi << 8));
+    } else {
+      row[c0 / 2] = (uint8_t)lo;
+      row[c0 / 2 + 1] = (uint8_t)hi;
+    }
+  }
+}
+
+// Whole contract in one launch for rows <= NI * (NT / 8): one workgroup per
+// channel slice holds every row of its slice in registers (NI rows per
+// thread), reduces the extremes (lanes xor 8/16/32, then LDS across the
+// waves), writes scale and zero-point and stores the bins. The input is read
+// once.
+template <int NT, int NI>
+__global__ __launch_bounds__(NT) void rows_single_kernel(RowsVecArgs a) {
+  constexpr int RPS = NT / 8, NWAVE = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int sub = tid & 7, rsub = tid >> 3;
+  const int c0 = blockIdx.x * kSliceCh + sub * 4;
+  const bool cval = c0 < a.C;
+  const int cl = cval ? c0 : a.C - 4;
+  float4 x[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int64_t r = min((int64_t)(rsub + i * RPS), a.rows - 1);
+    x[i] = ld16f_stream(a.kv + r * a.stride + cl);
+  }
+  float mn[4], mx[4];
+  minmax4<NI>(x, mn, mx);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    mn[k] = allreduce_min_f<8, 64>(mn[k]);
+    mx[k] = allreduce_max_f<8, 64>(mx[k]);
+  }
+  __shared__ float4 s_mn[NWAVE][8], s_mx[NWAVE][8];
+  if (lane < 8) {
+    s_mn[wv][lane] = make_float4(mn[0], mn[1], mn[2], mn[3]);
+    s_mx[wv][lane] = make_float4(mx[0], mx[1], mx[2], mx[3]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    const float4 pm = s_mn[w][sub], px = s_mx[w][sub];
+    mn[0] = fminf(mn[0], pm.x); mx[0] = fmaxf(mx[0], px.x);
+    mn[1] = fminf(mn[1], pm.y); mx[1] = fmaxf(mx[1], px.y);
+    mn[2] = fminf(mn[2], pm.z); mx[2] = fmaxf(mx[2], px.z);
+    mn[3] = fminf(mn[3], pm.w); mx[3] = fmaxf(mx[3], px.w);
+  }
+  if (!cval) return;
+  float sc[4], zp[4], rc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    scale_zp(mn[k], mx[k], &sc[k], &zp[k]);
+    rc[k] = 1.0f / sc[k];
+  }
+  if (rsub == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      a.scale[c0 + k] = sc[k];
+      a.zp[c0 + k] = zp[k];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int r = rsub + i * RPS;
+    if (r < a.rows) store_bins4(a, r, c0, x[i], mn, sc, rc);
+  }
+}
+
+// Multi-pass form for more rows: tiles of kRowsTile rows; 256 threads cover
+// 32 rows of a slice per sweep, 8 sweeps per tile.
+constexpr int kVecSweeps = kRowsTile / (kRowsThreads / 8);
+
+// Pass 1: per-tile extremes, partial[tile * C + c] = (min, max).
+__global__ __launch_bounds__(kRowsThreads) void rows_minmax_vec_kernel(RowsVecArgs a,
+                                                                       float2* __restrict__ partial) {
+  constexpr int RPS = kRowsThreads / 8;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int sub = tid & 7, rsub = tid >> 3;
+  const int c0 = blockIdx.x * kSliceCh + sub * 4;
+  const bool cval = c0 < a.C;
+  const int cl = cval ? c0 : a.C - 4;
+  const int64_t r0 = (int64_t)blockIdx.y * kRowsTile;
+  const int64_t rlast = min(r0 + kRowsTile, a.rows) - 1;
+  float4 x[kVecSweeps];
+#pragma unroll
+  for (int i = 0; i < kVecSweeps; ++i) {
+    const int64_t r = min(r0 + rsub + i * RPS, rlast);
+    x[i] = ld16f_stream(a.kv + r * a.stride + cl);
+  }
+  float mn[4], mx[4];
+  minmax4<kVecSweeps>(x, mn, mx);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    mn[k] = allreduce_min_f<8, 64>(mn[k]);
+    mx[k] = allreduce_max_f<8, 64>(mx[k]);
+  }
+  __shared__ float4 s_mn[kRowsThreads / 64][8], s_mx[kRowsThreads / 64][8];
+  if (lane < 8) {
+    s_mn[wv][lane] = make_float4(mn[0], mn[1], mn[2], mn[3]);
+    s_mx[wv][lane] = make_float4(mx[0], mx[1], mx[2], mx[3]);
+  }
+  __syncthreads();
+  if (wv != 0 || lane >= 8 || !cval) return;
+#pragma unroll
+  for (int w = 1; w < kRowsThreads / 64; ++w) {
+    const float4 pm = s_mn[w][lane], px = s_mx[w][lane];
+    mn[0] = fminf(mn[0], pm.x); mx[0] = fmaxf(mx[0], px.x);
+    mn[1] = fminf(mn[1], pm.y); mx[1] = fmaxf(mx[1], px.y);
+    mn[2] = fminf(mn[2], pm.z); mx[2] = fmaxf(mx[2], px.z);
+    mn[3] = fminf(mn[3], pm.w); mx[3] = fmaxf(mx[3], px.w);
+  }
+  float2* dst = partial + (int64_t)blockIdx.y * a.C + c0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) dst[k] = make_float2(mn[k], mx[k]);
+}
+
+// Pass 2: one workgroup per 64 channels; wave w combines tiles w, w + 4, ...
+// (8 independent loads in flight per lane), the waves meet in LDS; writes
+// scale, zero-point and (min, scale) for pass 3.
+__global__ __launch_bounds__(kRowsThreads) void rows_finalize_vec_kernel(
+    const float2* __restrict__ partial, int n_tiles, int C, float* __restrict__ scale_out,
+    float* __restrict__ zp_out, float2* __restrict__ mn_scale) {
+  constexpr int NW = kRowsThreads / 64, U = 8;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  float mn = INFINITY, mx = -INFINITY;
+  if (c < C) {
+    for (int t0 = wv; t0 < n_tiles; t0 += NW * U) {
+      float2 p[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int t = min(t0 + u * NW, n_tiles - 1);
+        p[u] = partial[(int64_t)t * C + c];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        mn = fminf(mn, p[u].x);
+        mx = fmaxf(mx, p[u].y);
+      }
+    }
+  }
+  __shared__ float s_mn[NW][64], s_mx[NW][64];
+  s_mn[wv][lane] = mn;
+  s_mx[wv][lane] = mx;
+  __syncthreads();
+  if (wv != 0 || c >= C) return;
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    mn = fminf(mn, s_mn[w][lane]);
+    mx = fmaxf(mx, s_mx[w][lane]);
+  }
+  float s, z;
+  scale_zp(mn, mx, &s, &z);
+  scale_out[c] = s;
+  zp_out[c] = z;
+  mn_scale[c] = make_float2(mn, s);
+}
+
+// Pass 3: bins of one tile (layout of pass 1).
+__global__ __launch_bounds__(kRowsThreads) void rows_quantize_vec_kernel(
+    RowsVecArgs a, const float2* __restrict__ mn_scale) {
+  constexpr int RPS = kRowsThreads / 8;
+  const int tid = threadIdx.x, sub = tid & 7, rsub = tid >> 3;
+  const int c0 = blockIdx.x * kSliceCh + sub * 4;
+  if (c0 >= a.C) return;
+  const int64_t r0 = (int64_t)blockIdx.y * kRowsTile;
+  const int64_t rlast = min(r0 + kRowsTile, a.rows) - 1;
+  float4 x[kVecSweeps];
+#pragma unroll
+  for (int i = 0; i < kVecSweeps; ++i) {
+    const int64_t r = min(r0 + rsub + i * RPS, rlast);
+    x[i] = ld16f_stream(a.kv + r * a.stride + c0);
+  }
+  float mn[4], sc[4], rc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float2 m = mn_scale[c0 + k];
+    mn[k] = m.x;
+    sc[k] = m.y;
+    rc[k] = 1.0f / m.y;
+  }
+#pragma unroll
+  for (int i = 0; i < kVecSweeps; ++i) {
+    const int64_t r = r0 + rsub + i * RPS;
+    if (r <= rlast) store_bins4(a, r, c0, x[i], mn, sc, rc);
+  }
+}
+
+// Rows up to which the one-launch kernel runs (NI = 32 rows per thread of a
+// 512-thread workgroup: 128 registers of input).
+constexpr int kSingleThreads = 512;
+constexpr int64_t kSingleMaxRows = 32 * (kSingleThreads / 8);
+
+hipError_t launch_quantize_rows_vec(const RowsVecArgs& a, void* ws, hipStream_t st) {
+  const unsigned slices = (unsigned)((a.C + kSliceCh - 1) / kSliceCh);
+  if (a.rows <= kSingleMaxRows) {
+    const int64_t per = (a.rows + kSingleThreads / 8 - 1) / (kSingleThreads / 8);
+#define FDI4_RS(NI)                                                                       \
+  if (per <= NI) {                                                                        \
+    hipLaunchKernelGGL((rows_single_kernel<kSingleThreads, NI>), dim3(slices),            \
+                       dim3(kSingleThreads), 0, st, a);                                   \
+    return hipGetLastError();                                                             \
+  }
+    FDI4_RS(1) FDI4_RS(2) FDI4_RS(4) FDI4_RS(8) FDI4_RS(16) FDI4_RS(32)
+#undef FDI4_RS
+  }
+  const int64_t tiles = (a.rows + kRowsTile - 1) / kRowsTile;
+  float2* partial = reinterpret_cast<float2*>(ws);
+  float2* mn_scale = partial + tiles * a.C;
+  hipLaunchKernelGGL(rows_minmax_vec_kernel, dim3(slices, (unsigned)tiles), dim3(kRowsThreads), 0,
+                     st, a, partial);
+  hipLaunchKernelGGL(rows_finalize_vec_kernel, dim3((unsigned)((a.C + 63) / 64)),
+                     dim3(kRowsThreads), 0, st, partial, (int)tiles, a.C, a.scale, a.zp, mn_scale);
+  hipLaunchKernelGGL(rows_quantize_vec_kernel, dim3(slices, (unsigned)tiles), dim3(kRowsThreads),
+                     0, st, a, mn_scale);
+  return hipGetLastError();
+}
+
 size_t rows_workspace_bytes(int64_t rows, int C) {
   const int64_t tiles = (rows + kRowsTile - 1) / kRowsTile;
   return (size_t)(tiles * C + C) * sizeof(float2);
@@ -156,6 +434,22 @@ size_t rows_workspace_bytes(int64_t rows, int C) {
 hipError_t launch_quantize_rows(const float* kv, int64_t rows, int C, int64_t stride,
                                 uint8_t* q, int64_t q_stride, bool packed, float* scale_out,
                                 float* zp_out, void* ws, hipStream_t st) {
+  // 16-byte path when every row is 16-byte aligned and C is a multiple of 4.
+  if (C % 4 == 0 && stride % 4 == 0 && (reinterpret_cast<uintptr_t>(kv) & 15) == 0) {
+    RowsVecArgs va;
+    va.kv = kv;
+    va.rows = rows;
+    va.stride = stride;
+    va.C = C;
+    va.q = q;
+    va.q_stride = q_stride;
+    va.packed = packed ? 1 : 0;
+    const uintptr_t wmask = packed ? 1 : 3;
+    va.q_word = ((reinterpret_cast<uintptr_t>(q) | (uintptr_t)q_stride) & wmask) == 0;
+    va.scale = scale_out;
+    va.zp = zp_out;
+    return launch_quantize_rows_vec(va, ws, st);
+  }
   const int64_t tiles = (rows + kRowsTile - 1) / kRowsTile;
   float2* partial = reinterpret_cast<float2*>(ws);
   float2* mn_scale = partial + tiles * C;

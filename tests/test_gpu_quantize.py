@@ -18,9 +18,15 @@ def _ops():
 class TestRowsQuantizer:
     """The 2-D contract: one group over all rows (reference src/ops.py:111-161)."""
 
+    # Shapes on both sides of each kernel choice: scalar kernels (C % 4 != 0),
+    # the one-launch 16-byte kernel (rows <= 2048, every rows-per-thread
+    # instance, slice tails with C % 32 != 0) and the three-pass 16-byte form
+    # (rows > 2048, partial last tile, many tiles).
     @pytest.mark.parametrize("shape", [(1, 1), (1, 64), (255, 3), (256, 3), (257, 3),
                                        (1030, 8), (4096, 128), (512, 128), (32768, 128),
-                                       (3, 1000)])
+                                       (3, 1000), (5, 4), (64, 36), (65, 36), (129, 100),
+                                       (300, 128), (777, 64), (2048, 128), (2049, 128),
+                                       (2047, 4), (8191, 36), (70000, 100)])
     def test_bit_exact(self, shape):
         kv = np.random.RandomState(shape[0]).randn(*shape).astype(np.float32)
         q, scale, zp = _ops().quantize_int4(kv, backend="hip")
@@ -62,6 +68,42 @@ class TestRowsQuantizer:
             C.quantize_int4(torch.zeros(0, 4, device="cuda"))
         with pytest.raises(RuntimeError, match="2D"):
             C.quantize_int4(torch.zeros(4, device="cuda"))
+
+    @pytest.mark.parametrize("rows,cols,offset", [(300, 64, 0), (300, 64, 1), (3000, 128, 0),
+                                                  (3000, 128, 1), (17, 8, 0)])
+    def test_packed_rows_16_byte_path(self, rows, cols, offset):
+        """C % 4 == 0: the 16-byte kernels, packed into a pool view whose rows
+        are 2-byte aligned (offset 0: half-word stores) or not (byte stores)."""
+        import torch
+        kv = np.random.RandomState(rows + cols).randn(rows, cols).astype(np.float32)
+        nb = cols // 2
+        pool = torch.zeros(2, rows + 3, nb + 4, dtype=torch.uint8, device="cuda")
+        view = pool[1, 1:rows + 1, offset:offset + nb]
+        s = torch.zeros(cols, device="cuda")
+        z = torch.zeros(cols, device="cuda")
+        _ops()._C.quantize_rows_into(torch.from_numpy(kv).cuda(), view, s, z, True)
+        qr, sr, zr = quantize_int4_ref(kv)
+        got = pool.cpu().numpy()
+        np.testing.assert_array_equal(got[1, 1:rows + 1, offset:offset + nb], pack_int4(qr))
+        outside = got.copy()
+        outside[1, 1:rows + 1, offset:offset + nb] = 0
+        assert not outside.any()
+        np.testing.assert_array_equal(s.cpu().numpy(), sr)
+        np.testing.assert_array_equal(z.cpu().numpy(), zr)
+
+    def test_unpacked_rows_unaligned_output(self):
+        """Unpacked bins into a byte-offset view (4-byte stores not possible)."""
+        import torch
+        kv = np.random.RandomState(3).randn(500, 64).astype(np.float32)
+        pool = torch.zeros(501, 70, dtype=torch.uint8, device="cuda")
+        view = pool[1:, 3:67]
+        s = torch.zeros(64, device="cuda")
+        z = torch.zeros(64, device="cuda")
+        _ops()._C.quantize_rows_into(torch.from_numpy(kv).cuda(), view, s, z, False)
+        qr, _, _ = quantize_int4_ref(kv)
+        got = pool.cpu().numpy()
+        np.testing.assert_array_equal(got[1:, 3:67], qr)
+        assert not got[0].any() and not got[:, :3].any() and not got[:, 67:].any()
 
     def test_packed_rows_into_strided_view(self):
         import torch
