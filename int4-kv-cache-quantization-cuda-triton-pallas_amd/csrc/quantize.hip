@@ -215,17 +215,18 @@ __device__ __forceinline__ void store_bins4(const RowsVecArgs& a, int64_t r, int
   }
 }
 
-// Whole contract in one launch for rows <= NI * (NT / 8): one workgroup per
-// channel slice holds every row of its slice in registers (NI rows per
-// thread), reduces the extremes (lanes xor 8/16/32, then LDS across the
-// waves), writes scale and zero-point and stores the bins. The input is read
-// once.
-template <int NT, int NI>
+// Whole contract in one launch: one workgroup per slice of SW channels (SW/4
+// lanes per row, NT*4/SW rows per sweep) holds every row of its slice in
+// registers (NI rows per thread), reduces the extremes (lane butterflies over
+// the row bits, then LDS across the waves), writes scale and zero-point and
+// stores the bins. The input is read once. Narrow slices give small inputs
+// more workgroups (more CUs pulling data).
+template <int NT, int NI, int SW>
 __global__ __launch_bounds__(NT) void rows_single_kernel(RowsVecArgs a) {
-  constexpr int RPS = NT / 8, NWAVE = NT / 64;
+  constexpr int LPR = SW / 4, RPS = NT / LPR, NWAVE = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int sub = tid & 7, rsub = tid >> 3;
-  const int c0 = blockIdx.x * kSliceCh + sub * 4;
+  const int sub = tid % LPR, rsub = tid / LPR;
+  const int c0 = blockIdx.x * SW + sub * 4;
   const bool cval = c0 < a.C;
   const int cl = cval ? c0 : a.C - 4;
   float4 x[NI];
@@ -238,11 +239,11 @@ __global__ __launch_bounds__(NT) void rows_single_kernel(RowsVecArgs a) {
   minmax4<NI>(x, mn, mx);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    mn[k] = allreduce_min_f<8, 64>(mn[k]);
-    mx[k] = allreduce_max_f<8, 64>(mx[k]);
+    mn[k] = allreduce_min_f<LPR, 64>(mn[k]);
+    mx[k] = allreduce_max_f<LPR, 64>(mx[k]);
   }
-  __shared__ float4 s_mn[NWAVE][8], s_mx[NWAVE][8];
-  if (lane < 8) {
+  __shared__ float4 s_mn[NWAVE][LPR], s_mx[NWAVE][LPR];
+  if (lane < LPR) {
     s_mn[wv][lane] = make_float4(mn[0], mn[1], mn[2], mn[3]);
     s_mx[wv][lane] = make_float4(mx[0], mx[1], mx[2], mx[3]);
   }
@@ -396,23 +397,55 @@ __global__ __launch_bounds__(kRowsThreads) void rows_quantize_vec_kernel(
   }
 }
 
-// Rows up to which the one-launch kernel runs (NI = 32 rows per thread of a
-// 512-thread workgroup: 128 registers of input).
 constexpr int kSingleThreads = 512;
-constexpr int64_t kSingleMaxRows = 32 * (kSingleThreads / 8);
+
+// The one-launch kernel runs up to kSingleMaxRows rows; beyond, the three
+// passes are faster (GPU time of graph-replayed calls on MI355X, one launch
+// against three: 256 x 128 4.5 against 7.0 us, 1024 x 128 8.1 against 8.1,
+// 2048 x 128 12.3 against 8.5, 16384 x 128 63.9 against 10.7; C = 64 and
+// 1024 alike): its threads walk long columns of rows while the passes spread
+// every row count over the whole chip.
+constexpr int64_t kSingleMaxRows = 1024;
+
+// Slice width of the one-launch kernel: the widest of 32, 16, 8, 4 channels
+// that still gives kSingleMinGroups workgroups (else 4), and the rows per
+// thread it then needs (at most 16 within kSingleMaxRows); 0 beyond 16.
+constexpr int kSingleMinGroups = 64;
+
+void pick_single(int64_t rows, int C, int* sw, int* ni) {
+  int w = 4;
+  for (int c : {32, 16, 8})
+    if ((C + c - 1) / c >= kSingleMinGroups) { w = c; break; }
+  const int64_t rps = kSingleThreads / (w / 4);
+  const int64_t per = (rows + rps - 1) / rps;
+  *sw = w;
+  *ni = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : per <= 16 ? 16 : 0;
+}
+
+template <int SW>
+hipError_t launch_single(const RowsVecArgs& a, int ni, hipStream_t st) {
+  const dim3 grid((unsigned)((a.C + SW - 1) / SW)), blk(kSingleThreads);
+  switch (ni) {
+    case 1: hipLaunchKernelGGL((rows_single_kernel<kSingleThreads, 1, SW>), grid, blk, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((rows_single_kernel<kSingleThreads, 2, SW>), grid, blk, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((rows_single_kernel<kSingleThreads, 4, SW>), grid, blk, 0, st, a); break;
+    case 8: hipLaunchKernelGGL((rows_single_kernel<kSingleThreads, 8, SW>), grid, blk, 0, st, a); break;
+    default: hipLaunchKernelGGL((rows_single_kernel<kSingleThreads, 16, SW>), grid, blk, 0, st, a); break;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_quantize_rows_vec(const RowsVecArgs& a, void* ws, hipStream_t st) {
   const unsigned slices = (unsigned)((a.C + kSliceCh - 1) / kSliceCh);
-  if (a.rows <= kSingleMaxRows) {
-    const int64_t per = (a.rows + kSingleThreads / 8 - 1) / (kSingleThreads / 8);
-#define FDI4_RS(NI)                                                                       \
-  if (per <= NI) {                                                                        \
-    hipLaunchKernelGGL((rows_single_kernel<kSingleThreads, NI>), dim3(slices),            \
-                       dim3(kSingleThreads), 0, st, a);                                   \
-    return hipGetLastError();                                                             \
-  }
-    FDI4_RS(1) FDI4_RS(2) FDI4_RS(4) FDI4_RS(8) FDI4_RS(16) FDI4_RS(32)
-#undef FDI4_RS
+  int sw, ni;
+  pick_single(a.rows, a.C, &sw, &ni);
+  if (ni > 0 && a.rows <= kSingleMaxRows) {
+    switch (sw) {
+      case 32: return launch_single<32>(a, ni, st);
+      case 16: return launch_single<16>(a, ni, st);
+      case 8: return launch_single<8>(a, ni, st);
+      default: return launch_single<4>(a, ni, st);
+    }
   }
   const int64_t tiles = (a.rows + kRowsTile - 1) / kRowsTile;
   float2* partial = reinterpret_cast<float2*>(ws);
