@@ -88,7 +88,8 @@ const char* fdi4_error_string(int status);
  * Bit-exact with NumPy: round half to even, IEEE float32 division.
  * Replaces cu_quantize_int4 (reference csrc/flash_decode_int4.cu:228-247,
  * declared at csrc/bindings.cpp:17-18); same arguments. Takes a stream-ordered
- * temporary from hipMallocAsync for the row-tile partials. */
+ * temporary for the row-tile partials from a memory pool the library keeps on
+ * the stream's device (hipMallocFromPoolAsync). */
 int fdi4_quantize_int4(const float* kv, int num_rows, int num_channels, uint8_t* q_out,
                        float* scale_out, float* zp_out, hipStream_t stream);
 
@@ -142,8 +143,8 @@ int fdi4_append_paged(const float* k_new, int64_t kn_batch_stride, int64_t kn_he
  * value [nb, bs, D] fp32, block_lens [nb]; every (b, h) query attends the same
  * page stream; 1 <= D <= 256. Replaces cu_flash_decode_int4 (reference
  * csrc/flash_decode_int4.cu:249-284, declared at csrc/bindings.cpp:19-21).
- * Packs keys into a stream-ordered temporary from hipMallocAsync, then runs
- * the split-K decode. */
+ * Packs keys into a stream-ordered temporary from the library's memory pool on
+ * the stream's device, then runs the split-K decode. */
 int fdi4_flash_decode_int4(const float* query, const uint8_t* k_q, const float* k_scale,
                            const float* k_zp, const float* value, const int* block_lens,
                            int batch_size, int num_heads, int head_dim, int num_blocks,

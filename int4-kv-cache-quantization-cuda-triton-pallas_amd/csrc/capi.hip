@@ -10,6 +10,8 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 
 #include "../../include/fdi4.h"
 #include "fdi4_internal.hpp"
@@ -157,17 +159,36 @@ int check_cache(const fdi4_paged_cache* c, bool need_values) {
   return hipSuccess;
 }
 
-void set_pool_threshold(hipStream_t) {
-  static bool done = false;
-  if (done) return;
+// Stream-ordered temporaries of the two entry points that keep the
+// reference's argument lists (no workspace argument) come from a memory pool
+// this library creates on each device at first use and keeps until the
+// process ends; its release threshold keeps freed blocks for the next call.
+// The process's default pool is left as the caller configured it.
+hipError_t temp_alloc(void** ptr, size_t bytes, hipStream_t stream) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return;
-  hipMemPool_t pool;
-  if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-    uint64_t keep = UINT64_MAX;
-    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  static std::mutex mu;
+  static std::map<int, hipMemPool_t> pools;
+  hipMemPool_t pool = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = pools.find(dev);
+    if (it == pools.end()) {
+      hipMemPoolProps props = {};
+      props.allocType = hipMemAllocationTypePinned;
+      props.handleTypes = hipMemHandleTypeNone;
+      props.location.type = hipMemLocationTypeDevice;
+      props.location.id = dev;
+      if ((e = hipMemPoolCreate(&pool, &props)) != hipSuccess) return e;
+      uint64_t keep = UINT64_MAX;
+      (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+      pools[dev] = pool;
+    } else {
+      pool = it->second;
+    }
   }
-  done = true;
+  return hipMallocFromPoolAsync(ptr, bytes, pool, stream);
 }
 
 }  // namespace
@@ -205,9 +226,8 @@ int fdi4_quantize_int4(const float* kv, int num_rows, int num_channels, uint8_t*
   if (num_rows <= 0 || num_channels <= 0 || !kv || !q_out || !scale_out || !zp_out)
     return hipErrorInvalidValue;
   const size_t wsb = fdi4::rows_workspace_bytes(num_rows, num_channels);
-  set_pool_threshold(stream);
   void* ws = nullptr;
-  hipError_t e = hipMallocAsync(&ws, wsb, stream);
+  hipError_t e = temp_alloc(&ws, wsb, stream);
   if (e != hipSuccess) return e;
   int rc = fdi4_quantize_rows(kv, num_rows, num_channels, num_channels, q_out, num_channels, 0,
                               scale_out, zp_out, ws, wsb, stream);
@@ -611,9 +631,8 @@ int fdi4_flash_decode_int4(const float* query, const uint8_t* k_q, const float* 
     return hipErrorInvalidValue;
   const size_t wsb = fdi4_flash_decode_int4_workspace_bytes(batch_size, num_heads, head_dim,
                                                             num_blocks, block_size);
-  set_pool_threshold(stream);
   void* ws = nullptr;
-  hipError_t e = hipMallocAsync(&ws, wsb, stream);
+  hipError_t e = temp_alloc(&ws, wsb, stream);
   if (e != hipSuccess) return e;
   int rc = fdi4_flash_decode_int4_ws(query, k_q, k_scale, k_zp, value, block_lens, batch_size,
                                      num_heads, head_dim, num_blocks, block_size, output, ws, wsb,

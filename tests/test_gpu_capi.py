@@ -39,6 +39,47 @@ def test_quantize_int4_exact_reference_signature():
     np.testing.assert_array_equal(z.cpu().numpy(), zr)
 
 
+def _default_pool_release_threshold():
+    """Release threshold of the current device's default memory pool, read
+    through the HIP runtime (hipDeviceGetDefaultMemPool / hipMemPoolGetAttribute)."""
+    import torch
+    hip = ctypes.CDLL("libamdhip64.so")
+    pool = ctypes.c_void_p()
+    assert hip.hipDeviceGetDefaultMemPool(ctypes.byref(pool), torch.cuda.current_device()) == 0
+    value = ctypes.c_uint64()
+    release_threshold = 0x4  # hipMemPoolAttrReleaseThreshold
+    assert hip.hipMemPoolGetAttribute(pool, release_threshold, ctypes.byref(value)) == 0
+    return value.value
+
+
+def test_reference_signatures_use_library_pool_on_any_stream():
+    """The entry points without a workspace argument take their temporaries
+    from the library's own pool: repeated calls on the default and on a side
+    stream give the oracle's results, and the process's default pool keeps
+    the release threshold it had."""
+    import torch
+    from flash_decode_int4 import capi
+    lib = capi.load()
+    before = _default_pool_release_threshold()
+    kv = np.random.RandomState(5).randn(3000, 64).astype(np.float32)
+    qr, sr, zr = quantize_int4_ref(kv)
+    x = torch.from_numpy(kv).cuda()
+    side = torch.cuda.Stream()
+    for stream in (torch.cuda.current_stream(), side, side, torch.cuda.current_stream()):
+        q = torch.zeros(3000, 64, dtype=torch.uint8, device="cuda")
+        s = torch.zeros(64, device="cuda")
+        z = torch.zeros(64, device="cuda")
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            capi.check(lib.fdi4_quantize_int4(_ptr(x), 3000, 64, _ptr(q), _ptr(s), _ptr(z),
+                                              ctypes.c_void_p(stream.cuda_stream)))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(q.cpu().numpy(), qr)
+        np.testing.assert_array_equal(s.cpu().numpy(), sr)
+        np.testing.assert_array_equal(z.cpu().numpy(), zr)
+    assert _default_pool_release_threshold() == before
+
+
 def test_flash_decode_int4_exact_reference_signature():
     """fdi4_flash_decode_int4: the reference's cu_flash_decode_int4 argument list
     (unpacked keys, shared page stream)."""
