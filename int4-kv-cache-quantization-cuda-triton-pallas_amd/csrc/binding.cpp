@@ -7,6 +7,7 @@
 // torch's caching allocator, takes the current HIP stream and calls the C
 // functions, which enqueue asynchronously.
 
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
 
@@ -20,13 +21,20 @@ namespace {
 // The attention kernel's head_dim limit (reference csrc/bindings.cpp:13-15).
 constexpr int64_t kMaxHeadDim = 256;
 
+// The current stream of the current device; every entry point first makes
+// the device of its tensors current (DeviceGuard), so the work is enqueued
+// there whatever device the caller has current.
 hipStream_t stream() { return c10::hip::getCurrentHIPStream().stream(); }
+
+using DeviceGuard = c10::hip::OptionalHIPGuardMasqueradingAsCUDA;
 
 #define CHECK_DEV(x) TORCH_CHECK((x).is_cuda(), #x " must be a GPU (cuda device) tensor")
 #define CHECK_CONTIGUOUS(x) TORCH_CHECK((x).is_contiguous(), #x " must be contiguous")
 #define CHECK_INPUT(x) \
   CHECK_DEV(x);        \
   CHECK_CONTIGUOUS(x)
+#define CHECK_SAME_DEVICE(ref, x) \
+  TORCH_CHECK((x).device() == (ref).device(), #x " must be on the device of " #ref)
 
 void check_rc(int rc, const char* what) {
   TORCH_CHECK(rc == 0, what, " failed: ", fdi4_error_string(rc));
@@ -46,6 +54,7 @@ std::vector<torch::Tensor> quantize_int4(torch::Tensor kv) {
               kv.size(1), "]");
   TORCH_CHECK(kv.size(0) <= INT32_MAX && kv.size(1) <= INT32_MAX,
               "kv dimensions must fit in int32");
+  const DeviceGuard guard(kv.device());
   const int64_t rows = kv.size(0);
   const int c = (int)kv.size(1);
   auto q = torch::empty({rows, c}, kv.options().dtype(torch::kUInt8));
@@ -69,6 +78,10 @@ void quantize_rows_into(torch::Tensor kv, torch::Tensor q_out, torch::Tensor sca
   CHECK_DEV(q_out);
   CHECK_INPUT(scale_out);
   CHECK_INPUT(zp_out);
+  CHECK_SAME_DEVICE(kv, q_out);
+  CHECK_SAME_DEVICE(kv, scale_out);
+  CHECK_SAME_DEVICE(kv, zp_out);
+  const DeviceGuard guard(kv.device());
   TORCH_CHECK(kv.dim() == 2 && kv.stride(1) == 1, "kv must be 2D with contiguous rows");
   TORCH_CHECK(kv.scalar_type() == torch::kFloat32, "kv must be float32");
   TORCH_CHECK(kv.size(0) > 0 && kv.size(1) > 0, "kv must be non-empty");
@@ -101,6 +114,12 @@ torch::Tensor flash_decode_int4(torch::Tensor query, torch::Tensor k_q, torch::T
   CHECK_INPUT(k_zp);
   CHECK_INPUT(value);
   CHECK_INPUT(block_lens);
+  CHECK_SAME_DEVICE(query, k_q);
+  CHECK_SAME_DEVICE(query, k_scale);
+  CHECK_SAME_DEVICE(query, k_zp);
+  CHECK_SAME_DEVICE(query, value);
+  CHECK_SAME_DEVICE(query, block_lens);
+  const DeviceGuard guard(query.device());
   TORCH_CHECK(query.dim() == 3, "query must be 3D [batch, heads, head_dim]");
   TORCH_CHECK(k_q.dim() == 3, "k_q must be 3D [num_blocks, block_size, head_dim]");
   TORCH_CHECK(query.scalar_type() == torch::kFloat32, "query must be float32");
@@ -160,6 +179,8 @@ fdi4_paged_cache make_cache(const torch::Tensor& k_pages, const torch::Tensor* v
   CHECK_DEV(k_pages);
   CHECK_DEV(k_scale);
   CHECK_DEV(k_zp);
+  CHECK_SAME_DEVICE(k_pages, k_scale);
+  CHECK_SAME_DEVICE(k_pages, k_zp);
   TORCH_CHECK(k_pages.scalar_type() == torch::kUInt8 && k_pages.dim() == 4 &&
                   k_pages.stride(3) == 1,
               "k_pages must be uint8 [pages, kv_heads, page_rows, head_dim/2]");
@@ -178,6 +199,7 @@ fdi4_paged_cache make_cache(const torch::Tensor& k_pages, const torch::Tensor* v
   c.k_row_stride = k_pages.stride(2);
   if (v_pages) {
     CHECK_DEV(*v_pages);
+    CHECK_SAME_DEVICE(k_pages, *v_pages);
     TORCH_CHECK(v_pages->dim() == 4 && v_pages->size(0) == k_pages.size(0) &&
                     v_pages->size(1) == k_pages.size(1) && v_pages->size(2) == k_pages.size(2) &&
                     v_pages->size(3) == D && v_pages->stride(3) == 1,
@@ -203,6 +225,7 @@ fdi4_paged_cache make_cache(const torch::Tensor& k_pages, const torch::Tensor* v
   }
   if (page_table && page_table->defined()) {
     CHECK_DEV(*page_table);
+    CHECK_SAME_DEVICE(k_pages, *page_table);
     TORCH_CHECK(page_table->scalar_type() == torch::kInt32 && page_table->dim() == 2 &&
                     page_table->stride(1) == 1,
                 "page_table must be int32 [batch, max_pages] with contiguous rows");
@@ -212,6 +235,7 @@ fdi4_paged_cache make_cache(const torch::Tensor& k_pages, const torch::Tensor* v
   }
   if (seq_lens && seq_lens->defined()) {
     CHECK_DEV(*seq_lens);
+    CHECK_SAME_DEVICE(k_pages, *seq_lens);
     TORCH_CHECK(seq_lens->scalar_type() == torch::kInt32 && seq_lens->dim() == 1 &&
                     seq_lens->stride(0) == 1,
                 "seq_lens must be contiguous int32 [batch]");
@@ -219,6 +243,7 @@ fdi4_paged_cache make_cache(const torch::Tensor& k_pages, const torch::Tensor* v
   }
   if (page_lens && page_lens->defined()) {
     CHECK_DEV(*page_lens);
+    CHECK_SAME_DEVICE(k_pages, *page_lens);
     TORCH_CHECK(page_lens->scalar_type() == torch::kInt32 && page_lens->dim() == 2 &&
                     page_lens->stride(1) == 1,
                 "page_lens must be int32 [batch, max_pages] with contiguous rows");
@@ -253,8 +278,10 @@ void quantize_paged(torch::Tensor k, torch::Tensor seq_lens, torch::Tensor page_
   TORCH_CHECK(k_scale.size(0) == k.size(0) && k_scale.size(1) == k.size(1) && k_scale.size(2) >= G,
               "k_scale must be [batch, kv_heads, >= ceil(tokens/group_rows), head_dim]");
   const int64_t max_pages = page_table.size(1);
+  CHECK_SAME_DEVICE(k, k_pages);
   fdi4_paged_cache c = make_cache(k_pages, nullptr, k_scale, k_zp, page_table, seq_lens,
                                   c10::nullopt, group_rows / k_pages.size(2), max_pages);
+  const DeviceGuard guard(k.device());
   check_rc(fdi4_quantize_paged(k.data_ptr<float>(), (int)k.size(0), (int)k.size(2), k.stride(0),
                                k.stride(1), k.stride(2), (int)group_rows, &c, stream()),
            "quantize_paged");
@@ -288,8 +315,12 @@ void append_paged(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_stag
   const int64_t max_pages = page_table.size(1);
   TORCH_CHECK(k_scale.size(2) * (group_rows / k_pages.size(2)) >= max_pages,
               "k_scale has fewer than ceil(max_pages / pages_per_group) groups");
+  CHECK_SAME_DEVICE(k_new, v_new);
+  CHECK_SAME_DEVICE(k_new, k_stage);
+  CHECK_SAME_DEVICE(k_new, k_pages);
   fdi4_paged_cache c = make_cache(k_pages, &v_pages, k_scale, k_zp, page_table, seq_lens,
                                   c10::nullopt, group_rows / k_pages.size(2), max_pages);
+  const DeviceGuard guard(k_new.device());
   check_rc(fdi4_append_paged(k_new.data_ptr<float>(), k_new.stride(0), k_new.stride(1),
                              v_new.data_ptr(), v_new.stride(0), v_new.stride(1), (int)B,
                              k_stage.data_ptr<float>(), k_stage.stride(0), k_stage.stride(1),
@@ -307,8 +338,10 @@ torch::Tensor decode_paged(torch::Tensor query, torch::Tensor k_pages, torch::Te
   TORCH_CHECK(query.scalar_type() == torch::kFloat32 && query.dim() == 3 && query.stride(2) == 1,
               "query must be float32 [batch, heads, head_dim] with contiguous rows");
   TORCH_CHECK(query.size(2) == k_pages.size(3) * 2, "query head_dim must match the cache");
+  CHECK_SAME_DEVICE(query, k_pages);
   fdi4_paged_cache c = make_cache(k_pages, &v_pages, k_scale, k_zp, page_table, seq_lens,
                                   page_lens, pages_per_group, max_pages);
+  const DeviceGuard guard(query.device());
   const int B = (int)query.size(0), Hq = (int)query.size(1), D = (int)query.size(2);
   // Every row the kernel may index must exist: batch rows of the per-sequence
   // tensors, and one scale group per pages_per_group logical pages.
@@ -349,8 +382,10 @@ void decode_paged_partials(torch::Tensor query, torch::Tensor k_pages, torch::Te
               "query must be float32 [batch, heads, head_dim] with contiguous rows");
   TORCH_CHECK(query.size(2) == k_pages.size(3) * 2, "query head_dim must match the cache");
   TORCH_CHECK(num_splits >= 1, "num_splits must be >= 1");
+  CHECK_SAME_DEVICE(query, k_pages);
   fdi4_paged_cache c = make_cache(k_pages, &v_pages, k_scale, k_zp, page_table, seq_lens,
                                   page_lens, pages_per_group, max_pages);
+  const DeviceGuard guard(query.device());
   const int B = (int)query.size(0), Hq = (int)query.size(1), D = (int)query.size(2);
   if (k_scale.dim() == 4) {
     TORCH_CHECK(k_scale.size(0) >= B && k_scale.size(2) * pages_per_group >= max_pages,
@@ -363,6 +398,7 @@ void decode_paged_partials(torch::Tensor query, torch::Tensor k_pages, torch::Te
   if (page_lens && page_lens->defined())
     TORCH_CHECK(page_lens->size(0) >= B, "page_lens must have a row per sequence");
   TORCH_CHECK(Hq % k_pages.size(1) == 0, "query heads must be a multiple of kv_heads");
+  CHECK_SAME_DEVICE(query, partials);
   const size_t need = fdi4_decode_partials_bytes(B, Hq, D, (int)num_splits);
   TORCH_CHECK(partials.scalar_type() == torch::kUInt8 && (size_t)partials.numel() >= need,
               "partials must be a uint8 buffer of at least ", need, " bytes");
@@ -380,6 +416,7 @@ torch::Tensor merge_splits(torch::Tensor partials, int64_t batch, int64_t q_head
   TORCH_CHECK(need > 0 && partials.scalar_type() == torch::kUInt8 &&
                   (size_t)partials.numel() >= need,
               "partials must be a uint8 buffer of at least ", need, " bytes");
+  const DeviceGuard guard(partials.device());
   auto out = torch::empty({batch, q_heads, head_dim},
                           partials.options().dtype(torch::kFloat32));
   const size_t acc_bytes = (size_t)batch * q_heads * num_splits * head_dim * sizeof(float);
@@ -416,6 +453,7 @@ torch::Tensor pack_int4(torch::Tensor q, int64_t out_cols) {
   const int64_t rows = q.size(0);
   const int c = (int)q.size(1);
   if (out_cols <= 0) out_cols = (c + 1) / 2;
+  const DeviceGuard guard(q.device());
   auto out = torch::empty({rows, out_cols}, q.options());
   check_rc(fdi4_pack_int4(q.data_ptr<uint8_t>(), rows, c, q.stride(0), out.data_ptr<uint8_t>(),
                           out_cols, (int)out_cols, stream()),
@@ -447,6 +485,8 @@ void fake_quantize(torch::Tensor k, torch::Tensor out, int64_t block_size, int64
               "scale_op must be 0 (divide) or 1 (reciprocal)");
   TORCH_CHECK(k.size(0) <= 65535 && k.size(1) <= 65535 && k.size(2) <= INT32_MAX,
               "k has too many sequences, heads or positions");
+  CHECK_SAME_DEVICE(k, out);
+  const DeviceGuard guard(k.device());
   check_rc(fdi4_fake_quantize(k.data_ptr(), code, (int)k.size(0), (int)k.size(1), (int)k.size(2),
                               (int)k.size(3), k.stride(0), k.stride(1), k.stride(2),
                               out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
