@@ -1,7 +1,8 @@
-"""The path at the benchmark's full sizes (B8 H32 D128 T2048; B64 H32 D128
-T4096, a 4.3 GB value pool whose byte offsets pass 2^32; ragged B32 up to
-8192 tokens), through properties that do not depend on size plus sampled
-streams against the oracle:
+"""The path at the benchmark's full sizes (B8 H32 D128 T2048; the
+context-length sweep B8 H32 D128 at T = 512, 8192 and 32768, the last a
+4.3 GB value pool; B64 H32 D128 T4096, also a 4.3 GB pool whose byte offsets
+pass 2^32; ragged B32 up to 8192 tokens), through properties that do not
+depend on size plus sampled streams against the oracle:
 
 * the grouped quantizer is bit-exact on sampled (sequence, head) streams;
 * decoding is invariant, bit for bit, under a different physical page
@@ -68,7 +69,8 @@ def torch_index(mask):
     return torch.as_tensor(np.nonzero(mask)[0], device="cuda")
 
 
-@pytest.fixture(scope="module", params=["anchor", "llama", "ragged"])
+@pytest.fixture(scope="module",
+                params=["anchor", "sweep_512", "sweep_8192", "sweep_32768", "llama", "ragged"])
 def built(request):
     import torch
     st = _build(request.param)
