@@ -53,7 +53,7 @@ direction only (a sum for reads, a fill for writes); --no-pmc skips them (and
 must be given when this script itself runs under rocprofv3).
 
 Prints ONE JSON line. Options: --workload (anchor, sweep_512 ... llama,
-ragged), --splits, --value-dtype float16, --no-cpu, --no-pmc.
+ragged), --splits, --value-dtype float16|bfloat16, --no-cpu, --no-pmc.
 """
 
 import argparse
@@ -86,7 +86,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="anchor")
     p.add_argument("--splits", type=int, default=0, help="0 = the library's choice")
-    p.add_argument("--value-dtype", default="float32", choices=["float32", "float16"])
+    p.add_argument("--value-dtype", default="float32",
+                   choices=["float32", "float16", "bfloat16"])
     p.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     p.add_argument("--cpu-runs", type=int, default=3)
     p.add_argument("--no-pmc", action="store_true",
@@ -103,7 +104,7 @@ def build_sets(name, value_dtype, n_sets_hint=0, seq_lens=None):
     sets = []
     first = workloads.make_workload(name, seq_lens=seq_lens, value_dtype=value_dtype,
                                     backend="torch", seed=1234)
-    vbytes = 2 if value_dtype == "float16" else 4
+    vbytes = 4 if value_dtype == "float32" else 2
     set_bytes = workloads.decode_bytes(first["seq_lens"], first["heads"], first["head_dim"],
                                        vbytes, q_heads=first["q_heads"])
     if n_sets_hint:
@@ -372,7 +373,7 @@ def time_append(w, value_dtype, steps, warmup):
     out = {}
     g = torch.Generator(device="cuda")
     g.manual_seed(77)
-    vdt = torch.float16 if value_dtype == "float16" else torch.float32
+    vdt = getattr(torch, value_dtype)
     k = torch.randn(B, H, T, D, generator=g, device="cuda")
     v = torch.randn(B, H, T, D, generator=g, device="cuda").to(vdt)
     kn = torch.randn(B, H, D, generator=g, device="cuda")
@@ -480,13 +481,14 @@ def time_fake_quant(steps, warmup):
 def time_other_paths(args):
     """Decode timings of the paths beside the headline one, on their own
     workloads (inputs rotated past the Infinity Cache as for the headline):
-    fp16 value pages at the anchor shape, and grouped-query heads (B8, 8
-    kv-heads, 32 q-heads, 8192 tokens). Skipped when the headline workload is
-    already one of them."""
+    fp16 and bf16 value pages at the anchor shape, and grouped-query heads (B8,
+    8 kv-heads, 32 q-heads, 8192 tokens). Skipped when the headline workload
+    is already one of them."""
     import torch
     from flash_decode_int4 import workloads
     out = {}
-    cases = (("fp16_values", "anchor", "float16"), ("grouped_query", "gqa", "float32"))
+    cases = (("fp16_values", "anchor", "float16"), ("bf16_values", "anchor", "bfloat16"),
+             ("grouped_query", "gqa", "float32"))
     for key, name, vdt in cases:
         if name == args.workload and vdt == args.value_dtype:
             continue
@@ -813,7 +815,7 @@ def main():
 
     sets, set_bytes = build_sets(args.workload, args.value_dtype)
     w0 = sets[0]["w"]
-    vbytes = 2 if args.value_dtype == "float16" else 4
+    vbytes = 4 if args.value_dtype == "float32" else 2
     qbytes = workloads.quantize_bytes(w0["seq_lens"], w0["heads"], w0["head_dim"])
 
     # Correctness before timing: the timed two-call path equals the one-call
@@ -862,7 +864,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (f64 logit accumulation)" if vbytes == 4 else "f32 with f16 values",
+        "dtype": ("f32 (f64 logit accumulation)" if vbytes == 4 else
+                  f"f32 with {'f16' if args.value_dtype == 'float16' else 'bf16'} values"),
         "data": "synthetic N(0,1) q/K/V, seeded; keys quantized on the GPU; random page "
                 "permutation",
         "config": {

@@ -25,7 +25,9 @@ extern "C" {
 
 #define FDI4_ABI_VERSION 1
 
-enum fdi4_value_dtype { FDI4_V_F32 = 0, FDI4_V_F16 = 1 };
+enum fdi4_value_dtype { FDI4_V_F32 = 0, FDI4_V_F16 = 1, FDI4_V_BF16 = 2 };
+/* Element types of key tensors (fdi4_fake_quantize) and of the queries and
+ * outputs of fdi4_decode_paged_ex. */
 enum fdi4_key_dtype { FDI4_K_F32 = 0, FDI4_K_F16 = 1, FDI4_K_BF16 = 2 };
 enum fdi4_rounding { FDI4_ROUND_HALF_UP = 0, FDI4_ROUND_HALF_EVEN = 1 };
 enum fdi4_scale_op { FDI4_SCALE_DIVIDE = 0, FDI4_SCALE_RECIPROCAL = 1 };
@@ -36,7 +38,7 @@ enum fdi4_scale_op { FDI4_SCALE_DIVIDE = 0, FDI4_SCALE_RECIPROCAL = 1 };
  *             channel 2j+1 (high nibble); address of row r of physical page p,
  *             kv-head h: k_pages + p*k_page_stride + h*k_head_stride +
  *             r*k_row_stride (bytes). A row holds head_dim/2 bytes.
- *   v_pages   values (fp32 or fp16), same addressing in elements.
+ *   v_pages   values (fp32, fp16 or bf16), same addressing in elements.
  *   k_scale,  per-channel scale and zero-point of the scale group of logical
  *   k_zp      page lp of sequence b: element offset
  *             b*s_batch_stride + h*s_head_stride + (lp/pages_per_group)*s_group_stride
@@ -183,6 +185,18 @@ int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_
                       int64_t q_head_stride, const fdi4_paged_cache* cache, float* out,
                       int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* fdi4_decode_paged with queries and outputs of any element type
+ * (fdi4_key_dtype: FDI4_K_F32, FDI4_K_F16, FDI4_K_BF16). The queries are
+ * widened to float32 exactly, the arithmetic is that of fdi4_decode_paged,
+ * and each output element is rounded once, to nearest even, from its float32
+ * value. The fp16/bf16 query and output side of the cache's 16-bit storage
+ * (the reference stores fp16 values, src/vllm_integration.py:45, 55). */
+int fdi4_decode_paged_ex(const void* query, int query_dtype, int batch, int num_q_heads,
+                         int64_t q_batch_stride, int64_t q_head_stride,
+                         const fdi4_paged_cache* cache, void* out, int out_dtype,
+                         int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Bytes of the split partials for fdi4_decode_paged_partials: part_acc
  * float [B, Hq, S, D] at offset 0, then part_ml double [B, Hq, S, 2] = (m, l)

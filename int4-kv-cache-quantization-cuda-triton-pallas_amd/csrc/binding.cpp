@@ -162,7 +162,17 @@ torch::Tensor flash_decode_int4(torch::Tensor query, torch::Tensor k_q, torch::T
 int dtype_code(const torch::Tensor& v) {
   if (v.scalar_type() == torch::kFloat32) return FDI4_V_F32;
   if (v.scalar_type() == torch::kFloat16) return FDI4_V_F16;
-  TORCH_CHECK(false, "v_pages must be float32 or float16");
+  if (v.scalar_type() == torch::kBFloat16) return FDI4_V_BF16;
+  TORCH_CHECK(false, "v_pages must be float32, float16 or bfloat16");
+  return -1;
+}
+
+// Element type code (fdi4_key_dtype) of a query / output tensor.
+int elem_code(const torch::Tensor& t, const char* what) {
+  if (t.scalar_type() == torch::kFloat32) return FDI4_K_F32;
+  if (t.scalar_type() == torch::kFloat16) return FDI4_K_F16;
+  if (t.scalar_type() == torch::kBFloat16) return FDI4_K_BF16;
+  TORCH_CHECK(false, what, " must be float32, float16 or bfloat16");
   return -1;
 }
 
@@ -335,8 +345,9 @@ torch::Tensor decode_paged(torch::Tensor query, torch::Tensor k_pages, torch::Te
                            c10::optional<torch::Tensor> page_lens, int64_t pages_per_group,
                            int64_t max_pages, int64_t num_splits) {
   CHECK_DEV(query);
-  TORCH_CHECK(query.scalar_type() == torch::kFloat32 && query.dim() == 3 && query.stride(2) == 1,
-              "query must be float32 [batch, heads, head_dim] with contiguous rows");
+  const int qcode = elem_code(query, "query");
+  TORCH_CHECK(query.dim() == 3 && query.stride(2) == 1,
+              "query must be [batch, heads, head_dim] with contiguous rows");
   TORCH_CHECK(query.size(2) == k_pages.size(3) * 2, "query head_dim must match the cache");
   CHECK_SAME_DEVICE(query, k_pages);
   fdi4_paged_cache c = make_cache(k_pages, &v_pages, k_scale, k_zp, page_table, seq_lens,
@@ -361,9 +372,9 @@ torch::Tensor decode_paged(torch::Tensor query, torch::Tensor k_pages, torch::Te
   auto out = torch::empty({B, Hq, D}, query.options());
   const int splits = num_splits > 0 ? (int)num_splits : fdi4_decode_num_splits(B, Hq, &c);
   auto ws = workspace(query, fdi4_decode_workspace_bytes(B, Hq, D, splits));
-  check_rc(fdi4_decode_paged(query.data_ptr<float>(), B, Hq, query.stride(0), query.stride(1), &c,
-                             out.data_ptr<float>(), out.stride(0), out.stride(1), splits,
-                             ws.data_ptr(), ws.numel(), stream()),
+  check_rc(fdi4_decode_paged_ex(query.data_ptr(), qcode, B, Hq, query.stride(0), query.stride(1),
+                                &c, out.data_ptr(), qcode, out.stride(0), out.stride(1), splits,
+                                ws.data_ptr(), ws.numel(), stream()),
            "decode_paged");
   return out;
 }

@@ -146,7 +146,8 @@ int check_cache(const fdi4_paged_cache* c, bool need_values) {
       c->s_head_stride % 4 || c->s_group_stride % 4 || c->s_page_stride % 4)
     return hipErrorInvalidValue;
   if (need_values) {
-    if (!c->v_pages || (c->v_dtype != FDI4_V_F32 && c->v_dtype != FDI4_V_F16))
+    if (!c->v_pages ||
+        (c->v_dtype != FDI4_V_F32 && c->v_dtype != FDI4_V_F16 && c->v_dtype != FDI4_V_BF16))
       return hipErrorInvalidValue;
     const int veb = c->v_dtype == FDI4_V_F32 ? 4 : 2;
     if (!aligned(c->v_pages, 16) || (c->v_page_stride * veb) % 16 ||
@@ -370,7 +371,7 @@ int fdi4_merge_splits(const float* part_acc, const double* part_ml, int batch, i
   if (!valid_head_dim(head_dim) || batch > 65535 || num_q_heads > 65535)
     return hipErrorInvalidValue;
   return fdi4::launch_merge(part_acc, part_ml, batch, num_q_heads, head_dim, num_splits, out,
-                            out_batch_stride, out_head_stride, stream);
+                            FDI4_K_F32, out_batch_stride, out_head_stride, stream);
 }
 
 }  // extern "C"
@@ -386,12 +387,17 @@ hipError_t launch_decode_any(const DecodeArgs& a, int d, int v_dtype, int batch,
   return fdi4::launch_decode(a, d, v_dtype, batch, stream);
 }
 
-int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_batch_stride,
-                     int64_t q_head_stride, const fdi4_paged_cache* cache, int num_splits,
-                     DecodeArgs* a) {
+bool valid_elem_dtype(int dt) {
+  return dt == FDI4_K_F32 || dt == FDI4_K_F16 || dt == FDI4_K_BF16;
+}
+
+int make_decode_args(const void* query, int q_dtype, int batch, int num_q_heads,
+                     int64_t q_batch_stride, int64_t q_head_stride,
+                     const fdi4_paged_cache* cache, int num_splits, DecodeArgs* a) {
   int rc = check_cache(cache, true);
   if (rc != hipSuccess) return rc;
-  if (!query || batch <= 0 || num_q_heads <= 0) return hipErrorInvalidValue;
+  if (!query || batch <= 0 || num_q_heads <= 0 || !valid_elem_dtype(q_dtype))
+    return hipErrorInvalidValue;
   if (batch > 65535 || num_q_heads > 65535) return hipErrorInvalidValue;
   if (num_q_heads % cache->num_kv_heads) return hipErrorInvalidValue;
   if (cache->page_table && cache->pt_batch_stride < 0) return hipErrorInvalidValue;
@@ -401,6 +407,7 @@ int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_b
   int splits = num_splits > 0 ? num_splits : plan.splits;
   splits = std::max(1, std::min(splits, std::max(chunks, 1)));
   a->q = query;
+  a->q_dtype = q_dtype;
   a->q_b = q_batch_stride;
   a->q_h = q_head_stride;
   a->k_pages = cache->k_pages;
@@ -431,6 +438,7 @@ int make_decode_args(const float* query, int batch, int num_q_heads, int64_t q_b
   a->num_splits = splits;
   a->num_q_heads = num_q_heads;
   a->out = nullptr;
+  a->out_dtype = FDI4_K_F32;
   a->o_b = a->o_h = 0;
   a->ws_acc = nullptr;
   a->ws_ml = nullptr;
@@ -457,17 +465,23 @@ int carve_partials(void* workspace, size_t workspace_bytes, int batch, int hq, i
 
 extern "C" {
 
-int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_batch_stride,
-                      int64_t q_head_stride, const fdi4_paged_cache* cache, float* out,
-                      int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
-                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+int decode_paged_any(const void* query, int q_dtype, int batch, int num_q_heads,
+                     int64_t q_batch_stride, int64_t q_head_stride,
+                     const fdi4_paged_cache* cache, void* out, int out_dtype,
+                     int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
   DecodeArgs a;
-  int rc = make_decode_args(query, batch, num_q_heads, q_batch_stride, q_head_stride, cache,
-                            num_splits, &a);
+  int rc = make_decode_args(query, q_dtype, batch, num_q_heads, q_batch_stride, q_head_stride,
+                            cache, num_splits, &a);
   if (rc != hipSuccess) return rc;
-  if (!out) return hipErrorInvalidValue;
+  if (!out || !valid_elem_dtype(out_dtype)) return hipErrorInvalidValue;
   const int d = cache->head_dim;
   a.out = out;
+  a.out_dtype = out_dtype;
   a.o_b = out_batch_stride;
   a.o_h = out_head_stride;
   if (a.num_splits == 1) {
@@ -479,7 +493,30 @@ int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_
   hipError_t e = launch_decode_any(a, d, cache->v_dtype, batch, stream);
   if (e != hipSuccess) return e;
   return fdi4::launch_merge(a.ws_acc, a.ws_ml, batch, num_q_heads, d, a.num_splits, out,
-                            out_batch_stride, out_head_stride, stream);
+                            out_dtype, out_batch_stride, out_head_stride, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_batch_stride,
+                      int64_t q_head_stride, const fdi4_paged_cache* cache, float* out,
+                      int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return decode_paged_any(query, FDI4_K_F32, batch, num_q_heads, q_batch_stride, q_head_stride,
+                          cache, out, FDI4_K_F32, out_batch_stride, out_head_stride, num_splits,
+                          workspace, workspace_bytes, stream);
+}
+
+int fdi4_decode_paged_ex(const void* query, int query_dtype, int batch, int num_q_heads,
+                         int64_t q_batch_stride, int64_t q_head_stride,
+                         const fdi4_paged_cache* cache, void* out, int out_dtype,
+                         int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return decode_paged_any(query, query_dtype, batch, num_q_heads, q_batch_stride, q_head_stride,
+                          cache, out, out_dtype, out_batch_stride, out_head_stride, num_splits,
+                          workspace, workspace_bytes, stream);
 }
 
 int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
@@ -487,8 +524,8 @@ int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
                                const fdi4_paged_cache* cache, int num_splits, void* partials,
                                size_t partials_bytes, hipStream_t stream) {
   DecodeArgs a;
-  int rc = make_decode_args(query, batch, num_q_heads, q_batch_stride, q_head_stride, cache,
-                            num_splits, &a);
+  int rc = make_decode_args(query, FDI4_K_F32, batch, num_q_heads, q_batch_stride,
+                            q_head_stride, cache, num_splits, &a);
   if (rc != hipSuccess) return rc;
   if (a.num_splits != num_splits) return hipErrorInvalidValue;  // the layout must be exact
   rc = carve_partials(partials, partials_bytes, batch, num_q_heads, cache->head_dim, &a);

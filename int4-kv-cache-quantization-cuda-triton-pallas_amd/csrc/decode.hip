@@ -43,7 +43,7 @@ struct Geo {
   static constexpr int KW = KBL / 4;               // 32-bit words per lane per row
   static constexpr int TPW = 64 / LPT;             // key rows per sweep
   static constexpr int KLD = 16 / TPW;             // key sweeps per chunk
-  static constexpr int VEB = VDT == kVF32 ? 4 : 2; // bytes per value element
+  static constexpr int VEB = VDT == kVF32 ? 4 : 2; // bytes per value element (f16, bf16: 2)
   static constexpr int VCL = 16 / VEB;             // value channels per lane
   static constexpr int VPR = D / VCL;              // lanes per value row
   static constexpr int RPL = 64 / VPR;             // value rows per sweep
@@ -237,21 +237,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     for (int i = 0; i < G::VLD; ++i) {
       const int r = i * G::RPL + vrow;
       const float p = (r < cm.nval) ? p_s[w][r] : 0.f;
-      if constexpr (VDT == kVF32) {
-        acc[0] = __builtin_fmaf(p, u2f(cv[i].x), acc[0]);
-        acc[1] = __builtin_fmaf(p, u2f(cv[i].y), acc[1]);
-        acc[2] = __builtin_fmaf(p, u2f(cv[i].z), acc[2]);
-        acc[3] = __builtin_fmaf(p, u2f(cv[i].w), acc[3]);
-      } else {
-        const unsigned u[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
+      float vf[G::VCL];
+      widen_values<VDT>(cv[i], vf);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const _Float16 lo = __builtin_bit_cast(_Float16, (unsigned short)(u[k] & 0xFFFFu));
-          const _Float16 hi = __builtin_bit_cast(_Float16, (unsigned short)(u[k] >> 16));
-          acc[2 * k] = __builtin_fmaf(p, (float)lo, acc[2 * k]);
-          acc[2 * k + 1] = __builtin_fmaf(p, (float)hi, acc[2 * k + 1]);
-        }
-      }
+      for (int k = 0; k < G::VCL; ++k) acc[k] = __builtin_fmaf(p, vf[k], acc[k]);
     }
     __builtin_amdgcn_wave_barrier();
     }
@@ -266,7 +255,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   // overlaps the q load and the workgroup barrier, and waiting for q (the
   // oldest load) does not wait for the chunk.
   static_assert(D <= NT, "one query element per thread");
-  const float qv = (tid < D) ? a.q[(int64_t)b * a.q_b + (int64_t)h * a.q_h + tid] : 0.f;
+  const float qv =
+      (tid < D) ? load_elem(a.q, (int64_t)b * a.q_b + (int64_t)h * a.q_h + tid, a.q_dtype) : 0.f;
   const bool has_work = c < wc1;
   KVec<G::KW> ka[G::KLD], kb[G::KLD];
   U32x4 va[G::VLD], vb[G::VLD];
@@ -315,7 +305,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < WAVES; ++i) o = __builtin_fmaf(ew[i], acc_s[i][d], o);
     if (a.final_out) {
-      a.out[(int64_t)b * a.o_b + (int64_t)h * a.o_h + d] = o / fmaxf(l, 1e-10f);
+      store_elem(a.out, (int64_t)b * a.o_b + (int64_t)h * a.o_h + d, a.out_dtype,
+                 o / fmaxf(l, 1e-10f));
     } else {
       a.ws_acc[pi * D + d] = o;
     }
@@ -330,8 +321,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
 template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ ws_acc,
                                                   const double* __restrict__ ws_ml, int hq,
-                                                  int splits, float* __restrict__ out,
-                                                  int64_t o_b, int64_t o_h) {
+                                                  int splits, void* __restrict__ out,
+                                                  int out_dtype, int64_t o_b, int64_t o_h) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int64_t p0 = ((int64_t)b * hq + h) * splits;
   double ms = -INFINITY;
@@ -344,7 +335,7 @@ __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ ws_a
     o = __builtin_fmaf(e, ws_acc[(p0 + s) * D + d], o);
     l = __builtin_fmaf(e, (float)ws_ml[2 * (p0 + s) + 1], l);
   }
-  out[(int64_t)b * o_b + (int64_t)h * o_h + d] = o / fmaxf(l, 1e-10f);
+  store_elem(out, (int64_t)b * o_b + (int64_t)h * o_h + d, out_dtype, o / fmaxf(l, 1e-10f));
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hipStream_t st) {
@@ -358,17 +349,20 @@ hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hip
   FDI4_DEC(64, kVF16, 4) FDI4_DEC(128, kVF16, 4) FDI4_DEC(256, kVF16, 4)
   FDI4_DEC(64, kVF32, 8) FDI4_DEC(128, kVF32, 8) FDI4_DEC(256, kVF32, 8)
   FDI4_DEC(64, kVF16, 8) FDI4_DEC(128, kVF16, 8) FDI4_DEC(256, kVF16, 8)
+  FDI4_DEC(64, kVBF16, 4) FDI4_DEC(128, kVBF16, 4) FDI4_DEC(256, kVBF16, 4)
+  FDI4_DEC(64, kVBF16, 8) FDI4_DEC(128, kVBF16, 8) FDI4_DEC(256, kVBF16, 8)
 #undef FDI4_DEC
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_merge(const float* ws_acc, const double* ws_ml, int batch, int hq, int D,
-                        int splits, float* out, int64_t o_b, int64_t o_h, hipStream_t st) {
+                        int splits, void* out, int out_dtype, int64_t o_b, int64_t o_h,
+                        hipStream_t st) {
   dim3 grid(hq, batch);
 #define FDI4_MRG(DD)                                                                         \
   if (D == DD) {                                                                             \
     hipLaunchKernelGGL((merge_kernel<DD>), grid, dim3(DD), 0, st, ws_acc, ws_ml, hq, splits, \
-                       out, o_b, o_h);                                                       \
+                       out, out_dtype, o_b, o_h);                                            \
     return hipGetLastError();                                                                \
   }
   FDI4_MRG(64) FDI4_MRG(128) FDI4_MRG(256)

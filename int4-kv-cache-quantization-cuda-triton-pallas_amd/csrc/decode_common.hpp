@@ -28,6 +28,55 @@ __device__ __forceinline__ KVec<KW> load_k(const uint8_t* p) {
   return r;
 }
 
+// One element of a query or output tensor of type dt (EDtype), as float32:
+// float16 and bfloat16 widen exactly.
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dt) {
+  if (dt == kEF32) return static_cast<const float*>(p)[i];
+  const unsigned short u = static_cast<const unsigned short*>(p)[i];
+  if (dt == kEF16) return (float)__builtin_bit_cast(_Float16, u);
+  return __uint_as_float((unsigned)u << 16);
+}
+
+// float32 -> bfloat16 bits, round to nearest even (NaN stays a quiet NaN).
+__device__ __forceinline__ unsigned short bf16_rne(float x) {
+  const unsigned u = __float_as_uint(x);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (unsigned short)((u >> 16) | 0x0040u);
+  return (unsigned short)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Store x into element i of an output tensor of type dt, rounded to nearest
+// even for the 16-bit types.
+__device__ __forceinline__ void store_elem(void* p, int64_t i, int dt, float x) {
+  if (dt == kEF32) {
+    static_cast<float*>(p)[i] = x;
+  } else if (dt == kEF16) {
+    static_cast<_Float16*>(p)[i] = (_Float16)x;
+  } else {
+    static_cast<unsigned short*>(p)[i] = bf16_rne(x);
+  }
+}
+
+// Four values packed in 16 bytes of a value row as float32: float32 (4
+// channels), float16 or bfloat16 (8 channels, two per 32-bit word).
+template <int VDT>
+__device__ __forceinline__ void widen_values(const U32x4& v, float* f) {
+  if constexpr (VDT == kVF32) {
+    f[0] = u2f(v.x); f[1] = u2f(v.y); f[2] = u2f(v.z); f[3] = u2f(v.w);
+  } else {
+    const unsigned u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (VDT == kVF16) {
+        f[2 * k] = (float)__builtin_bit_cast(_Float16, (unsigned short)(u[k] & 0xFFFFu));
+        f[2 * k + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(u[k] >> 16));
+      } else {
+        f[2 * k] = __uint_as_float(u[k] << 16);
+        f[2 * k + 1] = __uint_as_float(u[k] & 0xFFFF0000u);
+      }
+    }
+  }
+}
+
 struct ChunkMeta {
   int64_t phys;
   int r0;

@@ -268,16 +268,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gqa_kernel(DecodeArgs a) {
         // -inf), and their value registers hold a copy of a valid row.
         const HeadP<HG> pr = p_s[w][r];
         float vf[G::VCL];
-        if constexpr (VDT == kVF32) {
-          vf[0] = u2f(cv[i].x); vf[1] = u2f(cv[i].y); vf[2] = u2f(cv[i].z); vf[3] = u2f(cv[i].w);
-        } else {
-          const unsigned u[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            vf[2 * k] = (float)__builtin_bit_cast(_Float16, (unsigned short)(u[k] & 0xFFFFu));
-            vf[2 * k + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(u[k] >> 16));
-          }
-        }
+        widen_values<VDT>(cv[i], vf);
 #pragma unroll
         for (int h = 0; h < HG; ++h) {
 #pragma unroll
@@ -300,7 +291,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gqa_kernel(DecodeArgs a) {
   for (int j = 0; j < QPT; ++j) {
     const int idx = tid + j * NT;
     qv[j] = (idx < HG * D)
-                ? a.q[(int64_t)b * a.q_b + (int64_t)(h0 + idx / D) * a.q_h + idx % D]
+                ? load_elem(a.q, (int64_t)b * a.q_b + (int64_t)(h0 + idx / D) * a.q_h + idx % D,
+                            a.q_dtype)
                 : 0.f;
   }
   const bool has_work = c < wc1;
@@ -357,7 +349,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gqa_kernel(DecodeArgs a) {
     const int hq = h0 + h;
     const int64_t pi = ((int64_t)b * a.num_q_heads + hq) * a.num_splits + split;
     if (a.final_out) {
-      a.out[(int64_t)b * a.o_b + (int64_t)hq * a.o_h + d] = o / fmaxf(l, 1e-10f);
+      store_elem(a.out, (int64_t)b * a.o_b + (int64_t)hq * a.o_h + d, a.out_dtype,
+                 o / fmaxf(l, 1e-10f));
     } else {
       a.ws_acc[pi * D + d] = o;
       if (d == 0) {
@@ -378,14 +371,15 @@ hipError_t launch_decode_gqa(const DecodeArgs& a, int D, int v_dtype, int batch,
   }
 #define FDI4_GQA_D(WW, HH)                                                               \
   FDI4_GQA(64, kVF32, WW, HH) FDI4_GQA(128, kVF32, WW, HH)                               \
-  FDI4_GQA(64, kVF16, WW, HH) FDI4_GQA(128, kVF16, WW, HH)
+  FDI4_GQA(64, kVF16, WW, HH) FDI4_GQA(128, kVF16, WW, HH)                               \
+  FDI4_GQA(64, kVBF16, WW, HH) FDI4_GQA(128, kVBF16, WW, HH)
   FDI4_GQA_D(4, 2) FDI4_GQA_D(8, 2) FDI4_GQA_D(4, 4) FDI4_GQA_D(8, 4)
   // Eight heads per workgroup at D=64 only, and D=256 with four waves only:
   // other shapes would spill registers or overflow LDS.
   FDI4_GQA(64, kVF32, 4, 8) FDI4_GQA(64, kVF32, 8, 8) FDI4_GQA(64, kVF16, 4, 8)
-  FDI4_GQA(64, kVF16, 8, 8)
+  FDI4_GQA(64, kVF16, 8, 8) FDI4_GQA(64, kVBF16, 4, 8) FDI4_GQA(64, kVBF16, 8, 8)
   FDI4_GQA(256, kVF32, 4, 2) FDI4_GQA(256, kVF32, 4, 4) FDI4_GQA(256, kVF16, 4, 2)
-  FDI4_GQA(256, kVF16, 4, 4)
+  FDI4_GQA(256, kVF16, 4, 4) FDI4_GQA(256, kVBF16, 4, 2) FDI4_GQA(256, kVBF16, 4, 4)
 #undef FDI4_GQA_D
 #undef FDI4_GQA
   return hipErrorInvalidValue;

@@ -302,16 +302,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
         // Rows past the valid count hold probability 0 and a copy of a valid row.
         const HeadF<HG> pr = p_s[w][i * G::RPL + vrow];
         float vf[G::VCL];
-        if constexpr (VDT == kVF32) {
-          vf[0] = u2f(cv[i].x); vf[1] = u2f(cv[i].y); vf[2] = u2f(cv[i].z); vf[3] = u2f(cv[i].w);
-        } else {
-          const unsigned u[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            vf[2 * k] = (float)__builtin_bit_cast(_Float16, (unsigned short)(u[k] & 0xFFFFu));
-            vf[2 * k + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(u[k] >> 16));
-          }
-        }
+        widen_values<VDT>(cv[i], vf);
 #pragma unroll
         for (int h = 0; h < HG; ++h)
 #pragma unroll
@@ -333,7 +324,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
   for (int j = 0; j < QPT; ++j) {
     const int idx = tid + j * NT;
     qv[j] = (idx < HG * D)
-                ? a.q[(int64_t)b * a.q_b + (int64_t)(h0 + idx / D) * a.q_h + idx % D]
+                ? load_elem(a.q, (int64_t)b * a.q_b + (int64_t)(h0 + idx / D) * a.q_h + idx % D,
+                            a.q_dtype)
                 : 0.f;
   }
   const bool has_work = c < wc1;
@@ -390,7 +382,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
     const int hq = h0 + h;
     const int64_t pi = ((int64_t)b * a.num_q_heads + hq) * a.num_splits + split;
     if (a.final_out) {
-      a.out[(int64_t)b * a.o_b + (int64_t)hq * a.o_h + d] = o / fmaxf(l, 1e-10f);
+      store_elem(a.out, (int64_t)b * a.o_b + (int64_t)hq * a.o_h + d, a.out_dtype,
+                 o / fmaxf(l, 1e-10f));
     } else {
       a.ws_acc[pi * D + d] = o;
       if (d == 0) {
@@ -411,7 +404,8 @@ hipError_t launch_decode_mfma(const DecodeArgs& a, int D, int v_dtype, int batch
   }
 #define FDI4_MF_H(WW, HH)                                                                 \
   FDI4_MF(64, kVF32, WW, HH) FDI4_MF(128, kVF32, WW, HH)                                  \
-  FDI4_MF(64, kVF16, WW, HH) FDI4_MF(128, kVF16, WW, HH)
+  FDI4_MF(64, kVF16, WW, HH) FDI4_MF(128, kVF16, WW, HH)                                  \
+  FDI4_MF(64, kVBF16, WW, HH) FDI4_MF(128, kVBF16, WW, HH)
   FDI4_MF_H(4, 2) FDI4_MF_H(8, 2) FDI4_MF_H(4, 4) FDI4_MF_H(8, 4)
   // Eight heads per workgroup.
   FDI4_MF_H(4, 8) FDI4_MF_H(8, 8)

@@ -8,7 +8,10 @@
 
 namespace fdi4 {
 
-enum VDtype : int { kVF32 = 0, kVF16 = 1 };
+enum VDtype : int { kVF32 = 0, kVF16 = 1, kVBF16 = 2 };
+
+// Element types of queries and outputs (the codes of fdi4_key_dtype).
+enum EDtype : int { kEF32 = 0, kEF16 = 1, kEBF16 = 2 };
 
 // Grouped paged quantizer: keys [B, H, T, D] (any strides, channel stride 1)
 // into packed pages and group scales.
@@ -46,7 +49,8 @@ struct AppendArgs {
 
 // Split-K paged decode.
 struct DecodeArgs {
-  const float* q;
+  const void* q;
+  int q_dtype;                          // EDtype of q
   int64_t q_b, q_h;                     // elements
   const uint8_t* k_pages;
   int64_t k_page, k_head, k_row;        // bytes
@@ -66,7 +70,8 @@ struct DecodeArgs {
   int waves;                            // wave64s per workgroup (4 or 8)
   int heads_per_wg;                     // q-heads per workgroup (1: per-head kernel)
   int mfma;                             // int8 matrix-core kernel (D = 64 or 128)
-  float* out;
+  void* out;
+  int out_dtype;                        // EDtype of out
   int64_t o_b, o_h;
   float* ws_acc;                        // [B, Hq, S, D]
   double* ws_ml;                        // [B, Hq, S, 2] = (m, l)
@@ -109,7 +114,8 @@ hipError_t launch_decode_mfma(const DecodeArgs& a, int D, int v_dtype, int batch
                               hipStream_t st);
 
 hipError_t launch_merge(const float* ws_acc, const double* ws_ml, int batch, int hq, int D,
-                        int splits, float* out, int64_t o_b, int64_t o_h, hipStream_t st);
+                        int splits, void* out, int out_dtype, int64_t o_b, int64_t o_h,
+                        hipStream_t st);
 
 hipError_t launch_fake_quant(const FakeQuantArgs& a, int key_dtype, int rounding, int batch,
                              int heads, hipStream_t st);

@@ -15,6 +15,7 @@ c_int, c_int32, c_int64, c_size_t, c_void_p = (ctypes.c_int, ctypes.c_int32, cty
 
 V_F32 = 0
 V_F16 = 1
+V_BF16 = 2
 K_F32, K_F16, K_BF16 = 0, 1, 2
 ROUND_HALF_UP, ROUND_HALF_EVEN = 0, 1
 SCALE_DIVIDE, SCALE_RECIPROCAL = 0, 1
@@ -72,6 +73,9 @@ SIGNATURES = {
     "fdi4_decode_paged": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64,
                                   ctypes.POINTER(PagedCache), c_void_p, c_int64, c_int64, c_int,
                                   c_void_p, c_size_t, c_void_p]),
+    "fdi4_decode_paged_ex": (c_int, [c_void_p, c_int, c_int, c_int, c_int64, c_int64,
+                                     ctypes.POINTER(PagedCache), c_void_p, c_int, c_int64,
+                                     c_int64, c_int, c_void_p, c_size_t, c_void_p]),
     "fdi4_decode_partials_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "fdi4_decode_paged_partials": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64,
                                            ctypes.POINTER(PagedCache), c_int, c_void_p,

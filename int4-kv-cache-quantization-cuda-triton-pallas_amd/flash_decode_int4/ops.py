@@ -268,11 +268,13 @@ def flash_decode_paged(query, k_pages, v_pages, k_scale, k_zp, page_table, seq_l
                        max_pages: Optional[int] = None):
     """Split-K fused INT4 flash decoding over the paged layout (all GPU tensors).
 
-    query float32 [B, Hq, D]; k_pages uint8 [P, Hkv, page_rows, D/2]; v_pages
-    float32 or float16 [P, Hkv, page_rows, D]; k_scale/k_zp [B, Hkv, G, D];
-    page_table int32 [B, max_pages] (or None for identity); seq_lens int32 [B]
-    (or None with page_lens). q-head h reads kv-head h // (Hq // Hkv).
-    Returns float32 [B, Hq, D] on the GPU.
+    query float32, float16 or bfloat16 [B, Hq, D]; k_pages uint8 [P, Hkv,
+    page_rows, D/2]; v_pages float32, float16 or bfloat16 [P, Hkv, page_rows,
+    D]; k_scale/k_zp [B, Hkv, G, D]; page_table int32 [B, max_pages] (or None
+    for identity); seq_lens int32 [B] (or None with page_lens). q-head h reads
+    kv-head h // (Hq // Hkv). Returns [B, Hq, D] on the GPU in the query's
+    dtype: float32 arithmetic, 16-bit queries widened exactly, one rounding
+    (to nearest even) of each output element.
     """
     _require_device(None)
     page_rows = k_pages.shape[2]

@@ -160,7 +160,7 @@ class INT4PagedSequenceCache:
     writes one token per sequence per step on the device.
 
       k_pages    uint8 [num_pages, kv_heads, page_rows, D/2]  nibble-packed keys
-      v_pages    float32 or float16 [num_pages, kv_heads, page_rows, D]
+      v_pages    float32, float16 or bfloat16 [num_pages, kv_heads, page_rows, D]
       k_scale    float32 [max_seqs, kv_heads, max_groups, D]  (and k_zp)
       page_table int32 [max_seqs, max_pages_per_seq]
       seq_lens   int32 [max_seqs]
@@ -184,8 +184,8 @@ class INT4PagedSequenceCache:
             raise ValueError(f"head_dim must be 64, 128 or 256, got {head_dim}")
         if group_rows not in (64, 128, 256) or group_rows % page_rows:
             raise ValueError("group_rows must be 64, 128 or 256 and a multiple of page_rows")
-        if value_dtype not in ("float32", "float16"):
-            raise ValueError("value_dtype must be float32 or float16")
+        if value_dtype not in ("float32", "float16", "bfloat16"):
+            raise ValueError("value_dtype must be float32, float16 or bfloat16")
         if min(num_pages, num_kv_heads, max_seqs, max_seq_len, page_rows) < 1:
             raise ValueError("sizes must be positive")
         self.num_pages, self.num_kv_heads, self.head_dim = num_pages, num_kv_heads, head_dim
@@ -193,7 +193,7 @@ class INT4PagedSequenceCache:
         self.max_pages_per_seq = (max_seq_len + page_rows - 1) // page_rows
         groups = (self.max_pages_per_seq * page_rows + group_rows - 1) // group_rows
         dev = torch.device("cuda")
-        vdt = torch.float16 if value_dtype == "float16" else torch.float32
+        vdt = getattr(torch, value_dtype)
         H, D = num_kv_heads, head_dim
         self.k_pages = torch.zeros(num_pages, H, page_rows, D // 2, dtype=torch.uint8, device=dev)
         self.v_pages = torch.zeros(num_pages, H, page_rows, D, dtype=vdt, device=dev)
@@ -302,7 +302,8 @@ class INT4PagedSequenceCache:
     def step(self, k_new, v_new, query, num_splits: int = 0):
         """One decode step on the device alone: append (k_new, v_new) [B,
         kv_heads, D] at each sequence's length, advance the lengths on the
-        device, attend with query [B, Hq, D]; returns float32 [B, Hq, D].
+        device, attend with query [B, Hq, D] (float32, float16 or bfloat16);
+        returns [B, Hq, D] in the query's dtype.
         No host bookkeeping happens, so the call can be captured in a HIP
         graph and replayed: the pages must already be mapped (reserve), and
         lengths() reflects the steps only after sync_lengths()."""
@@ -322,8 +323,9 @@ class INT4PagedSequenceCache:
     # ---- reads -------------------------------------------------------------
 
     def decode(self, query, num_splits: int = 0):
-        """Fused INT4 attention of query [B, Hq, D] (float32, Hq a multiple of
-        kv_heads) over sequences 0..B-1; returns float32 [B, Hq, D]."""
+        """Fused INT4 attention of query [B, Hq, D] (float32, float16 or bfloat16;
+        Hq a multiple of kv_heads) over sequences 0..B-1; returns [B, Hq, D] in
+        the query's dtype (float32 arithmetic, one rounding at the end)."""
         B = query.shape[0]
         return ops.flash_decode_paged(query, self.k_pages, self.v_pages, self.k_scale[:B],
                                       self.k_zp[:B], self.page_table[:B], self.seq_lens[:B],

@@ -119,6 +119,8 @@ def make_workload(name=None, *, batch=None, heads=None, head_dim=None, tokens=No
         rng = np.random.RandomState(seed)
         out["q"] = rng.randn(batch, q_heads, head_dim).astype(np.float32)
         k = rng.randn(batch, heads, tmax, head_dim).astype(np.float32)
+        if value_dtype == "bfloat16":
+            raise ValueError("bfloat16 values need backend='torch' (NumPy has no bfloat16)")
         out["v_pages"] = rng.randn(P, heads, PAGE_ROWS, head_dim).astype(value_dtype)
         if rope:
             k = rope_rotate(k)
@@ -135,7 +137,7 @@ def make_workload(name=None, *, batch=None, heads=None, head_dim=None, tokens=No
     g.manual_seed(seed)
     out["q"] = torch.randn(batch, q_heads, head_dim, generator=g, device=dev)
     k = torch.randn(batch, heads, tmax, head_dim, generator=g, device=dev)
-    vdt = torch.float16 if value_dtype == "float16" else torch.float32
+    vdt = getattr(torch, value_dtype)
     out["v_pages"] = torch.randn(P, heads, PAGE_ROWS, head_dim, generator=g, device=dev).to(vdt)
     if rope:
         half = head_dim // 2

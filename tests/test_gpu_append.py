@@ -20,6 +20,12 @@ def _cache(**kw):
     return INT4PagedSequenceCache(**kw)
 
 
+def _stored(v, vdtype):
+    """float32 values as the cache stores them (rounded to vdtype), widened back."""
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(v)).to(getattr(torch, vdtype)).float().numpy()
+
+
 def _check_against_oracle(cache, streams, lens, group, vdtype):
     """streams[b] = (K [H, n, D] float32, V [H, n, D]) of sequence b's tokens."""
     B = len(streams)
@@ -45,13 +51,13 @@ def _check_against_oracle(cache, streams, lens, group, vdtype):
             np.testing.assert_array_equal(kp[table[b, lp], :, :n],
                                           pack_int4(qr[b, :, lp * 16:lp * 16 + n]))
             np.testing.assert_array_equal(vp[table[b, lp], :, :n],
-                                          vb[:, lp * 16:lp * 16 + n].astype(vdtype)
-                                          .astype(np.float32))
+                                          _stored(vb[:, lp * 16:lp * 16 + n], vdtype))
     return table
 
 
 @pytest.mark.parametrize("D,group,vdtype,H", [(128, 128, "float32", 2), (64, 64, "float16", 3),
-                                              (256, 256, "float32", 1)])
+                                              (256, 256, "float32", 1),
+                                              (128, 128, "bfloat16", 2)])
 def test_append_equals_whole_sequence_quantization(D, group, vdtype, H):
     import torch
     rng = np.random.RandomState(D + group)
@@ -68,7 +74,7 @@ def test_append_equals_whole_sequence_quantization(D, group, vdtype, H):
     for b in range(B):
         k0[b, :, :lens0[b]] = streams[b][0][:, :lens0[b]]
         v0[b, :, :lens0[b]] = streams[b][1][:, :lens0[b]]
-    vt = torch.float16 if vdtype == "float16" else torch.float32
+    vt = getattr(torch, vdtype)
     cache.prefill(torch.from_numpy(k0).cuda(), torch.from_numpy(v0).cuda().to(vt), lens0)
     for s in range(steps):
         kn = np.stack([streams[b][0][:, lens0[b] + s] for b in range(B)])

@@ -282,6 +282,47 @@ class TestPagedDecode:
         o32, o64 = paged_decode_ref(*args), paged_decode_f64(*args)
         assert np.abs(out - o32).max() <= max(TOL, 1.25 * np.abs(o32 - o64).max())
 
+    @pytest.mark.parametrize("D", [64, 128, 256])
+    def test_bf16_values(self, D):
+        """bfloat16 value pages: the oracle gets the identical widened values."""
+        import torch
+        from flash_decode_int4.workloads import make_workload
+        w = make_workload(batch=3, heads=2, head_dim=D, seq_lens=[500, 0, 1031], seed=D + 1)
+        q_t, kp, v_t, s, z, pt, sl = _paged_device(w, value_dtype=torch.bfloat16)
+        out = _ops().flash_decode_paged(q_t, kp, v_t, s, z, pt, sl).cpu().numpy()
+        args = _oracle_inputs(w, kp, s, z, v=v_t.float().cpu().numpy())
+        o32, o64 = paged_decode_ref(*args), paged_decode_f64(*args)
+        assert np.abs(out - o32).max() <= max(TOL, 1.25 * np.abs(o32 - o64).max())
+        assert np.all(out[1] == 0.0)
+
+    @pytest.mark.parametrize("qdtype", ["float16", "bfloat16"])
+    @pytest.mark.parametrize("vdtype,rep,splits", [("float32", 1, 1), ("float16", 1, 3),
+                                                   ("bfloat16", 4, 1), ("float16", 4, 2),
+                                                   ("bfloat16", 1, 5)])
+    def test_16_bit_queries_and_outputs(self, qdtype, vdtype, rep, splits):
+        """A float16 / bfloat16 query gives an output of its own type equal, bit
+        for bit, to the float32 decode of the widened query rounded to that type
+        (one rounding, to nearest even, in the final store or in the merge),
+        for the per-head and the grouped kernels, with and without splits; and
+        the float32 result is within the oracle's tolerance."""
+        import torch
+        from flash_decode_int4.workloads import make_workload
+        w = make_workload(batch=3, heads=2, head_dim=128, seq_lens=[700, 0, 1500], seed=rep + 40)
+        q_t, kp, v_t, s, z, pt, sl = _paged_device(w, value_dtype=getattr(torch, vdtype))
+        dt = getattr(torch, qdtype)
+        g = torch.Generator("cuda").manual_seed(rep + splits)
+        q16 = torch.randn(3, 2 * rep, 128, device="cuda", generator=g).to(dt)
+        out16 = _ops().flash_decode_paged(q16, kp, v_t, s, z, pt, sl, num_splits=splits)
+        assert out16.dtype == dt
+        out32 = _ops().flash_decode_paged(q16.float(), kp, v_t, s, z, pt, sl, num_splits=splits)
+        assert torch.equal(out16, out32.to(dt))
+        assert bool((out16[1] == 0).all())
+        args = list(_oracle_inputs(w, kp, s, z, v=v_t.float().cpu().numpy()))
+        args[0] = q16.float().cpu().numpy()
+        o32, o64 = paged_decode_ref(*args), paged_decode_f64(*args)
+        got = out32.cpu().numpy()
+        assert np.abs(got - o32).max() <= max(TOL, 1.25 * np.abs(o32 - o64).max())
+
     def test_deterministic_bitwise(self):
         from flash_decode_int4.workloads import make_workload
         w = make_workload(batch=2, heads=4, head_dim=128, seq_lens=[2048, 999], seed=14)
@@ -311,13 +352,16 @@ class TestGroupedQueryHeads:
         (128, 8, "float16", [1200, 5, 0], 0),
         (128, 16, "float16", [300, 2000], 0),  # two workgroups of 8 per kv-head
         (64, 8, "float16", [700, 33], 3),
+        (128, 4, "bfloat16", [900, 17], 0),
+        (64, 8, "bfloat16", [300, 1100], 2),
+        (256, 4, "bfloat16", [129, 700], 0),
     ])
     def test_matches_oracle(self, D, rep, vdtype, lens, splits):
         import torch
         from flash_decode_int4.workloads import make_workload
         hkv = 2
         w = make_workload(batch=len(lens), heads=hkv, head_dim=D, seq_lens=lens, seed=D + rep)
-        vt = torch.float16 if vdtype == "float16" else None
+        vt = None if vdtype == "float32" else getattr(torch, vdtype)
         q_t, kp, v_t, s, z, pt, sl = _paged_device(w, value_dtype=vt)
         g = torch.Generator("cuda").manual_seed(rep)
         q = torch.randn(len(lens), hkv * rep, D, device="cuda", generator=g)
@@ -334,7 +378,7 @@ class TestGroupedQueryHeads:
 
     @pytest.mark.parametrize("D,rep,vdtype", [(128, 4, None), (64, 8, None), (128, 2, None),
                                               (128, 8, None), (128, 8, "float16"),
-                                              (64, 4, "float16")])
+                                              (64, 4, "float16"), (128, 4, "bfloat16")])
     def test_matrix_core_equals_vector_kernel(self, monkeypatch, D, rep, vdtype):
         """The int8 matrix-core kernel's logits are exact up to the 41-bit
         rounding of q*s; it agrees with the vector grouped kernel (fp64
@@ -343,7 +387,7 @@ class TestGroupedQueryHeads:
         from flash_decode_int4.workloads import make_workload
         w = make_workload(batch=2, heads=2, head_dim=D, seq_lens=[1500, 333], seed=D + rep)
         q_t, kp, v_t, s, z, pt, sl = _paged_device(
-            w, value_dtype=torch.float16 if vdtype else None)
+            w, value_dtype=getattr(torch, vdtype) if vdtype else None)
         q = torch.randn(2, 2 * rep, D, device="cuda", generator=torch.Generator("cuda").manual_seed(7))
         mfma = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=2)
         monkeypatch.setenv("FDI4_DECODE_MFMA", "0")

@@ -25,10 +25,13 @@ def _cache(value_dtype):
                                   max_seq_len=1024, value_dtype=value_dtype)
 
 
-@pytest.mark.parametrize("value_dtype,q_heads,steps", [("float32", 4, 6), ("float16", 16, 5)])
-def test_graph_replayed_steps_equal_eager_steps(value_dtype, q_heads, steps):
+@pytest.mark.parametrize("value_dtype,q_heads,steps,q_dtype", [
+    ("float32", 4, 6, "float32"), ("float16", 16, 5, "float32"),
+    ("bfloat16", 8, 4, "bfloat16"), ("float16", 4, 4, "float16")])
+def test_graph_replayed_steps_equal_eager_steps(value_dtype, q_heads, steps, q_dtype):
     import torch
     vdt = getattr(torch, value_dtype)
+    qdt = getattr(torch, q_dtype)
     B, H, D, T0 = 3, 4, 128, 400
     lens0 = [100, 127, 300]                      # 127: the first step closes a group
     g = torch.Generator(device="cuda").manual_seed(5)
@@ -40,7 +43,8 @@ def test_graph_replayed_steps_equal_eager_steps(value_dtype, q_heads, steps):
         c.reserve(B, steps + 1)
     k_in = [torch.randn(B, H, D, device="cuda", generator=g) for _ in range(steps + 1)]
     v_in = [torch.randn(B, H, D, device="cuda", generator=g).to(vdt) for _ in range(steps + 1)]
-    q_in = [torch.randn(B, q_heads, D, device="cuda", generator=g) for _ in range(steps + 1)]
+    q_in = [torch.randn(B, q_heads, D, device="cuda", generator=g).to(qdt)
+            for _ in range(steps + 1)]
 
     # Step 0 eagerly on both (warm-up outside the capture), then capture step 1.
     eager_out = [eager.step(k_in[0], v_in[0], q_in[0])]
@@ -87,8 +91,12 @@ def test_graph_replayed_steps_equal_eager_steps(value_dtype, q_heads, steps):
         npg = (n[b] + 15) // 16
         got = kp[table[b, :npg]].transpose(1, 0, 2, 3).reshape(H, npg * 16, D // 2)[:, :n[b]]
         np.testing.assert_array_equal(got, pack_int4(qr[b, :, :n[b]]))
-    args = (q_in[steps].cpu().numpy(), kp, vp, sc, eager.k_zp[:B].cpu().numpy(), table,
+    args = (q_in[steps].float().cpu().numpy(), kp, vp, sc, eager.k_zp[:B].cpu().numpy(), table,
             np.array(n, np.int32))
     o32, o64 = paged_decode_ref(*args), paged_decode_f64(*args)
-    got = eager_out[steps].cpu().numpy()
+    # A 16-bit query's output is the float32 decode of the widened query,
+    # rounded once; the float32 decode is what the oracle bounds.
+    full = eager.decode(q_in[steps].float())
+    assert torch.equal(eager_out[steps], full.to(qdt))
+    got = full.cpu().numpy()
     assert np.abs(got - o32).max() <= max(TOL, 1.25 * np.abs(o32 - o64).max())
