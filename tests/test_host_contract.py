@@ -267,3 +267,24 @@ class TestCABI:
         big.v_row_stride = 1 << 25
         assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
                                      None, 0, None) == bad
+
+    def test_typed_decode_rejects_unknown_element_types(self):
+        """fdi4_decode_paged_ex: query and output types are 0, 1, 2 (float32,
+        float16, bfloat16); value pages fp32, fp16 or bf16; anything else is
+        refused before any device call."""
+        from flash_decode_int4 import capi
+        lib = capi.load()
+        bad = 1
+        ok_cache = capi.PagedCache(head_dim=128, page_rows=16, num_kv_heads=1, pages_per_group=8,
+                                   max_pages=8, num_pages=8, k_pages=256, k_scale=256, k_zp=256,
+                                   k_page_stride=1024, k_row_stride=64, v_pages=256,
+                                   v_dtype=capi.V_BF16, v_page_stride=2048, v_row_stride=128,
+                                   s_group_stride=128, seq_lens=256)
+        q = ctypes.c_void_p(256)
+        for q_dtype, o_dtype in ((3, 0), (0, 3), (-1, 1), (2, 7)):
+            assert lib.fdi4_decode_paged_ex(q, q_dtype, 1, 1, 128, 128, ctypes.byref(ok_cache),
+                                            q, o_dtype, 128, 128, 1, None, 0, None) == bad
+        ok_cache.v_dtype = 3
+        assert lib.fdi4_decode_paged_ex(q, 1, 1, 1, 128, 128, ctypes.byref(ok_cache), q, 1,
+                                        128, 128, 1, None, 0, None) == bad
+        assert capi.V_BF16 == 2 and capi.K_BF16 == 2
