@@ -397,19 +397,94 @@ __global__ __launch_bounds__(kRowsThreads) void rows_quantize_vec_kernel(
   }
 }
 
+// Passes 2 and 3 in one launch when there are at most kFusedMaxTiles tiles
+// (rows <= 16384; 2048 x 128 7.2 against 8.5 us for three launches, 16384 x
+// 128 8.6 against 10.7, graph-replayed GPU time):
+// every workgroup reduces the tile extremes of its 32 channels itself (at
+// most 64 x 32 partials, L2-resident after the first reads), the workgroups
+// of tile 0 write scale and zero-point, and each quantizes its tile. The
+// tile's rows are loaded first so that their latency overlaps the reduction.
+constexpr int kFusedMaxTiles = 64;
+
+__global__ __launch_bounds__(kRowsThreads) void rows_finalize_quantize_vec_kernel(
+    RowsVecArgs a, const float2* __restrict__ partial, int n_tiles) {
+  constexpr int RPS = kRowsThreads / 8, TG = kRowsThreads / kSliceCh;
+  const int tid = threadIdx.x, sub = tid & 7, rsub = tid >> 3;
+  const int c0 = blockIdx.x * kSliceCh + sub * 4;
+  const bool cval = c0 < a.C;
+  const int cl = cval ? c0 : a.C - 4;
+  const int64_t r0 = (int64_t)blockIdx.y * kRowsTile;
+  const int64_t rlast = min(r0 + kRowsTile, a.rows) - 1;
+  float4 x[kVecSweeps];
+#pragma unroll
+  for (int i = 0; i < kVecSweeps; ++i) {
+    const int64_t r = min(r0 + rsub + i * RPS, rlast);
+    x[i] = ld16f_stream(a.kv + r * a.stride + cl);
+  }
+  // Thread t reduces channel t % 32 of the slice over tiles t / 32 + TG * j.
+  const int ch = blockIdx.x * kSliceCh + (tid % kSliceCh);
+  const int chl = min(ch, a.C - 1);
+  float mn = INFINITY, mx = -INFINITY;
+  float2 p[kFusedMaxTiles / TG];
+#pragma unroll
+  for (int j = 0; j < kFusedMaxTiles / TG; ++j) {
+    const int t = min(tid / kSliceCh + TG * j, n_tiles - 1);
+    p[j] = partial[(int64_t)t * a.C + chl];
+  }
+#pragma unroll
+  for (int j = 0; j < kFusedMaxTiles / TG; ++j) {
+    mn = fminf(mn, p[j].x);
+    mx = fmaxf(mx, p[j].y);
+  }
+  __shared__ float s_mn[TG][kSliceCh], s_mx[TG][kSliceCh];
+  s_mn[tid / kSliceCh][tid % kSliceCh] = mn;
+  s_mx[tid / kSliceCh][tid % kSliceCh] = mx;
+  __syncthreads();
+  if (!cval) return;
+  float cmn[4], sc[4], zp[4], rc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < TG; ++g) {
+      lo = fminf(lo, s_mn[g][sub * 4 + k]);
+      hi = fmaxf(hi, s_mx[g][sub * 4 + k]);
+    }
+    cmn[k] = lo;
+    scale_zp(lo, hi, &sc[k], &zp[k]);
+    rc[k] = 1.0f / sc[k];
+  }
+  if (blockIdx.y == 0 && rsub == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      a.scale[c0 + k] = sc[k];
+      a.zp[c0 + k] = zp[k];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kVecSweeps; ++i) {
+    const int64_t r = r0 + rsub + i * RPS;
+    if (r <= rlast) store_bins4(a, r, c0, x[i], cmn, sc, rc);
+  }
+}
+
 constexpr int kSingleThreads = 512;
 
-// The one-launch kernel runs up to kSingleMaxRows rows; beyond, the three
-// passes are faster (GPU time of graph-replayed calls on MI355X, one launch
-// against three: 256 x 128 4.5 against 7.0 us, 1024 x 128 8.1 against 8.1,
-// 2048 x 128 12.3 against 8.5, 16384 x 128 63.9 against 10.7; C = 64 and
-// 1024 alike): its threads walk long columns of rows while the passes spread
-// every row count over the whole chip.
-constexpr int64_t kSingleMaxRows = 1024;
+// The one-launch kernel runs up to kSingleMaxRows rows (kSingleMaxRowsNarrow
+// for rows of at most kNarrowC channels); beyond, the passes are faster. GPU
+// time of graph-replayed calls on MI355X, one launch against extremes +
+// fused finalize-and-bins: 128 x 128 3.4 against 5.3 us, 512 x 128 6.1
+// against 6.1, 768 x 128 7.1 against 6.4, 1024 x 128 8.1 against 6.6 (C = 64
+// and 1024 alike); 1024 x 8 3.5 against 6.5. The one-launch kernel's threads
+// walk long columns of narrow slices, which for wide rows fetch each line
+// from several workgroups; the passes spread any row count over the chip.
+constexpr int64_t kSingleMaxRows = 512;
+constexpr int64_t kSingleMaxRowsNarrow = 1024;
+constexpr int kNarrowC = 16;
 
 // Slice width of the one-launch kernel: the widest of 32, 16, 8, 4 channels
 // that still gives kSingleMinGroups workgroups (else 4), and the rows per
-// thread it then needs (at most 16 within kSingleMaxRows); 0 beyond 16.
+// thread it then needs (at most 16 within the row limits); 0 beyond 16.
 constexpr int kSingleMinGroups = 64;
 
 void pick_single(int64_t rows, int C, int* sw, int* ni) {
@@ -439,7 +514,8 @@ hipError_t launch_quantize_rows_vec(const RowsVecArgs& a, void* ws, hipStream_t 
   const unsigned slices = (unsigned)((a.C + kSliceCh - 1) / kSliceCh);
   int sw, ni;
   pick_single(a.rows, a.C, &sw, &ni);
-  if (ni > 0 && a.rows <= kSingleMaxRows) {
+  const int64_t single_max = a.C <= kNarrowC ? kSingleMaxRowsNarrow : kSingleMaxRows;
+  if (ni > 0 && a.rows <= single_max) {
     switch (sw) {
       case 32: return launch_single<32>(a, ni, st);
       case 16: return launch_single<16>(a, ni, st);
@@ -452,6 +528,11 @@ hipError_t launch_quantize_rows_vec(const RowsVecArgs& a, void* ws, hipStream_t 
   float2* mn_scale = partial + tiles * a.C;
   hipLaunchKernelGGL(rows_minmax_vec_kernel, dim3(slices, (unsigned)tiles), dim3(kRowsThreads), 0,
                      st, a, partial);
+  if (tiles <= kFusedMaxTiles) {
+    hipLaunchKernelGGL(rows_finalize_quantize_vec_kernel, dim3(slices, (unsigned)tiles),
+                       dim3(kRowsThreads), 0, st, a, partial, (int)tiles);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(rows_finalize_vec_kernel, dim3((unsigned)((a.C + 63) / 64)),
                      dim3(kRowsThreads), 0, st, partial, (int)tiles, a.C, a.scale, a.zp, mn_scale);
   hipLaunchKernelGGL(rows_quantize_vec_kernel, dim3(slices, (unsigned)tiles), dim3(kRowsThreads),

@@ -19,16 +19,20 @@ class TestRowsQuantizer:
     """The 2-D contract: one group over all rows (reference src/ops.py:111-161)."""
 
     # Shapes on both sides of each kernel choice: scalar kernels (C % 4 != 0),
-    # the one-launch 16-byte kernel (rows <= 1024, every slice width and
-    # rows-per-thread instance, slice tails with C % 32 != 0) and the
-    # three-pass 16-byte form (rows > 1024, partial last tile, many tiles).
+    # the one-launch 16-byte kernel (rows <= 512, or <= 1024 for C <= 16;
+    # every slice width and rows-per-thread instance, slice tails with
+    # C % 32 != 0), the two-pass form (up to 16384 rows: extremes, then
+    # finalize fused with the bins) and the three-pass form (more rows;
+    # partial last tile, many tiles).
     @pytest.mark.parametrize("shape", [(1, 1), (1, 64), (255, 3), (256, 3), (257, 3),
                                        (1030, 8), (4096, 128), (512, 128), (32768, 128),
                                        (3, 1000), (5, 4), (64, 36), (65, 36), (129, 100),
                                        (300, 128), (777, 64), (2048, 128), (2049, 128),
                                        (2047, 4), (8191, 36), (70000, 100), (1024, 128),
                                        (1025, 128), (1024, 4), (8, 4096), (1000, 2048),
-                                       (200, 512), (40, 256), (100, 1024)])
+                                       (200, 512), (40, 256), (100, 1024), (16384, 64),
+                                       (16385, 64), (512, 64), (513, 64), (1024, 16),
+                                       (1025, 16), (300, 4096)])
     def test_bit_exact(self, shape):
         kv = np.random.RandomState(shape[0]).randn(*shape).astype(np.float32)
         q, scale, zp = _ops().quantize_int4(kv, backend="hip")
