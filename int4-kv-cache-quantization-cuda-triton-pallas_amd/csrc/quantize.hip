@@ -397,15 +397,20 @@ __global__ __launch_bounds__(kRowsThreads) void rows_quantize_vec_kernel(
   }
 }
 
-// Passes 2 and 3 in one launch when there are at most kFusedMaxTiles tiles
-// (rows <= 16384; 2048 x 128 7.2 against 8.5 us for three launches, 16384 x
-// 128 8.6 against 10.7, graph-replayed GPU time):
+// Passes 2 and 3 in one launch for few tiles (graph-replayed GPU time on
+// MI355X against three launches: 2048 x 128 7.2 against 8.5 us, 16384 x 128
+// 8.6 against 10.7, 32768 x 128 12.4 against 14.8):
 // every workgroup reduces the tile extremes of its 32 channels itself (at
-// most 64 x 32 partials, L2-resident after the first reads), the workgroups
+// most MAXT x 32 partials, L2-resident after the first reads), the workgroups
 // of tile 0 write scale and zero-point, and each quantizes its tile. The
 // tile's rows are loaded first so that their latency overlaps the reduction.
-constexpr int kFusedMaxTiles = 64;
+// Every workgroup reads all tiles' partials of its slice, tiles^2 * C * 8 / 32
+// bytes in all, so the fused form is limited to 64 tiles, or 128 for rows of
+// at most kFused128MaxC channels (at C = 1024 and 128 tiles three launches
+// are faster: 67.2 against 68.8 us).
+constexpr int kFused128MaxC = 256;
 
+template <int MAXT>
 __global__ __launch_bounds__(kRowsThreads) void rows_finalize_quantize_vec_kernel(
     RowsVecArgs a, const float2* __restrict__ partial, int n_tiles) {
   constexpr int RPS = kRowsThreads / 8, TG = kRowsThreads / kSliceCh;
@@ -425,14 +430,14 @@ __global__ __launch_bounds__(kRowsThreads) void rows_finalize_quantize_vec_kerne
   const int ch = blockIdx.x * kSliceCh + (tid % kSliceCh);
   const int chl = min(ch, a.C - 1);
   float mn = INFINITY, mx = -INFINITY;
-  float2 p[kFusedMaxTiles / TG];
+  float2 p[MAXT / TG];
 #pragma unroll
-  for (int j = 0; j < kFusedMaxTiles / TG; ++j) {
+  for (int j = 0; j < MAXT / TG; ++j) {
     const int t = min(tid / kSliceCh + TG * j, n_tiles - 1);
     p[j] = partial[(int64_t)t * a.C + chl];
   }
 #pragma unroll
-  for (int j = 0; j < kFusedMaxTiles / TG; ++j) {
+  for (int j = 0; j < MAXT / TG; ++j) {
     mn = fminf(mn, p[j].x);
     mx = fmaxf(mx, p[j].y);
   }
@@ -528,8 +533,13 @@ hipError_t launch_quantize_rows_vec(const RowsVecArgs& a, void* ws, hipStream_t 
   float2* mn_scale = partial + tiles * a.C;
   hipLaunchKernelGGL(rows_minmax_vec_kernel, dim3(slices, (unsigned)tiles), dim3(kRowsThreads), 0,
                      st, a, partial);
-  if (tiles <= kFusedMaxTiles) {
-    hipLaunchKernelGGL(rows_finalize_quantize_vec_kernel, dim3(slices, (unsigned)tiles),
+  if (tiles <= 64) {
+    hipLaunchKernelGGL(rows_finalize_quantize_vec_kernel<64>, dim3(slices, (unsigned)tiles),
+                       dim3(kRowsThreads), 0, st, a, partial, (int)tiles);
+    return hipGetLastError();
+  }
+  if (tiles <= 128 && a.C <= kFused128MaxC) {
+    hipLaunchKernelGGL(rows_finalize_quantize_vec_kernel<128>, dim3(slices, (unsigned)tiles),
                        dim3(kRowsThreads), 0, st, a, partial, (int)tiles);
     return hipGetLastError();
   }

@@ -21,9 +21,9 @@ class TestRowsQuantizer:
     # Shapes on both sides of each kernel choice: scalar kernels (C % 4 != 0),
     # the one-launch 16-byte kernel (rows <= 512, or <= 1024 for C <= 16;
     # every slice width and rows-per-thread instance, slice tails with
-    # C % 32 != 0), the two-pass form (up to 16384 rows: extremes, then
-    # finalize fused with the bins) and the three-pass form (more rows;
-    # partial last tile, many tiles).
+    # C % 32 != 0), the two-pass form (up to 64 tiles of 256 rows, or 128
+    # for C <= 256: extremes, then finalize fused with the bins) and the
+    # three-pass form (more rows; partial last tile, many tiles).
     @pytest.mark.parametrize("shape", [(1, 1), (1, 64), (255, 3), (256, 3), (257, 3),
                                        (1030, 8), (4096, 128), (512, 128), (32768, 128),
                                        (3, 1000), (5, 4), (64, 36), (65, 36), (129, 100),
@@ -32,7 +32,8 @@ class TestRowsQuantizer:
                                        (1025, 128), (1024, 4), (8, 4096), (1000, 2048),
                                        (200, 512), (40, 256), (100, 1024), (16384, 64),
                                        (16385, 64), (512, 64), (513, 64), (1024, 16),
-                                       (1025, 16), (300, 4096)])
+                                       (1025, 16), (300, 4096), (20000, 100), (32769, 128),
+                                       (17000, 512)])
     def test_bit_exact(self, shape):
         kv = np.random.RandomState(shape[0]).randn(*shape).astype(np.float32)
         q, scale, zp = _ops().quantize_int4(kv, backend="hip")
