@@ -37,10 +37,11 @@ __device__ __forceinline__ float load_elem(const void* p, int64_t i, int dt) {
   return __uint_as_float((unsigned)u << 16);
 }
 
-// float32 -> bfloat16 bits, round to nearest even (NaN stays a quiet NaN).
+// float32 -> bfloat16 bits, round to nearest even; NaN becomes the canonical
+// quiet NaN 0x7FC0 (as torch's conversion gives).
 __device__ __forceinline__ unsigned short bf16_rne(float x) {
   const unsigned u = __float_as_uint(x);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (unsigned short)((u >> 16) | 0x0040u);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (unsigned short)0x7FC0u;
   return (unsigned short)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 

@@ -323,6 +323,26 @@ class TestPagedDecode:
         got = out32.cpu().numpy()
         assert np.abs(got - o32).max() <= max(TOL, 1.25 * np.abs(o32 - o64).max())
 
+    @pytest.mark.parametrize("qdtype", ["float16", "bfloat16"])
+    def test_16_bit_output_rounding_at_the_range_ends(self, qdtype):
+        """One live token: the output is that token's value row exactly, so
+        the 16-bit output must be torch's rounding of the row itself, here
+        values that overflow the 16-bit type, sit at its largest finite value,
+        fall in its subnormal range or below it."""
+        import torch
+        from flash_decode_int4.workloads import make_workload
+        w = make_workload(batch=1, heads=1, head_dim=64, seq_lens=[1], seed=3)
+        q_t, kp, v_t, s, z, pt, sl = _paged_device(w)
+        row = torch.tensor([3.4e38, -3.4e38, 3.3895e38, 65504.0, 65520.0, -65520.0, 1e-40,
+                            -1e-40, 6e-8, 3e-8, 1.0 + 2.0 ** -9, 1.0 + 2.0 ** -8, 0.0, 1.5],
+                           device="cuda")
+        v_t[pt[0, 0], 0, 0, :] = 0.0
+        v_t[pt[0, 0], 0, 0, :row.numel()] = row
+        dt = getattr(torch, qdtype)
+        out = _ops().flash_decode_paged(q_t.to(dt), kp, v_t, s, z, pt, sl)
+        want = v_t[pt[0, 0], 0, 0, :].to(dt)
+        assert torch.equal(out[0, 0].view(torch.int16), want.view(torch.int16))
+
     def test_deterministic_bitwise(self):
         from flash_decode_int4.workloads import make_workload
         w = make_workload(batch=2, heads=4, head_dim=128, seq_lens=[2048, 999], seed=14)
