@@ -135,3 +135,63 @@ def test_capacity_and_shapes_are_checked():
         c.append(torch.zeros(1, 2, 64, device="cuda"), torch.zeros(1, 2, 64, device="cuda"))
     c.free(0)
     assert c.lengths()[0] == 0 and c.memory_stats()["pages"] == 0
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_prefill_and_appends(seed):
+    """Seeded random caches (head dims, page sizes 8-32, scale groups 64-256,
+    1-3 kv-heads, value dtypes, prefill lengths on and next to page and group
+    edges, 1-40 appended tokens): pages, scales and values equal the grouped
+    quantizer applied to each whole sequence, bit for bit."""
+    import torch
+    rng = np.random.RandomState(500 + seed)
+    D = int(rng.choice([64, 128, 256]))
+    H = int(rng.choice([1, 2, 3]))
+    B = int(rng.randint(1, 4))
+    page_rows = int(rng.choice([8, 16, 32]))
+    group = int(rng.choice([64, 128, 256]))
+    vdtype = str(rng.choice(["float32", "float16", "bfloat16"]))
+    steps = int(rng.randint(1, 41))
+    edges = [0, 1, page_rows - 1, page_rows, group - 1, group, group + 1, 2 * group - 3]
+    lens0 = [int(rng.choice(edges)) if rng.rand() < 0.7 else int(rng.randint(0, 400))
+             for _ in range(B)]
+    total = [n + steps for n in lens0]
+    streams = [(rng.randn(H, n, D).astype(np.float32), rng.randn(H, n, D).astype(np.float32))
+               for n in total]
+    cap = max(total) + page_rows
+    cache = _cache(num_pages=sum((n + page_rows) // page_rows + 1 for n in total) + 4,
+                   num_kv_heads=H, head_dim=D, max_seqs=B, max_seq_len=cap,
+                   page_rows=page_rows, group_rows=group, value_dtype=vdtype)
+    vt = getattr(torch, vdtype)
+    T0 = max(max(lens0), 1)
+    k0 = np.zeros((B, H, T0, D), np.float32)
+    v0 = np.zeros((B, H, T0, D), np.float32)
+    for b in range(B):
+        k0[b, :, :lens0[b]] = streams[b][0][:, :lens0[b]]
+        v0[b, :, :lens0[b]] = streams[b][1][:, :lens0[b]]
+    cache.prefill(torch.from_numpy(k0).cuda(), torch.from_numpy(v0).cuda().to(vt), lens0)
+    for s in range(steps):
+        kn = np.stack([streams[b][0][:, lens0[b] + s] for b in range(B)])
+        vn = np.stack([streams[b][1][:, lens0[b] + s] for b in range(B)])
+        cache.append(torch.from_numpy(kn).cuda(), torch.from_numpy(vn).cuda().to(vt))
+    # Compare through the cache's own page table, at its page size.
+    kk = np.zeros((B, H, max(total), D), np.float32)
+    for b in range(B):
+        kk[b, :, :total[b]] = streams[b][0]
+    qr, sr, zr = quantize_groups_ref(kk, np.array(total), group_size=group)
+    kp = cache.k_pages.cpu().numpy()
+    vp = cache.v_pages.float().cpu().numpy()
+    sc, zc = cache.k_scale.cpu().numpy(), cache.k_zp.cpu().numpy()
+    table = cache.page_table.cpu().numpy()
+    assert list(cache.seq_lens[:B].cpu().numpy()) == total
+    for b in range(B):
+        ng = (total[b] + group - 1) // group
+        np.testing.assert_array_equal(sc[b, :, :ng], sr[b, :, :ng])
+        np.testing.assert_array_equal(zc[b, :, :ng], zr[b, :, :ng])
+        for lp in range((total[b] + page_rows - 1) // page_rows):
+            n = min(page_rows, total[b] - lp * page_rows)
+            np.testing.assert_array_equal(kp[table[b, lp], :, :n],
+                                          pack_int4(qr[b, :, lp * page_rows:lp * page_rows + n]))
+            np.testing.assert_array_equal(
+                vp[table[b, lp], :, :n],
+                _stored(streams[b][1][:, lp * page_rows:lp * page_rows + n], vdtype))
