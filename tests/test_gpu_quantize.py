@@ -266,3 +266,40 @@ class TestQuantizerTies:
                 n = min(16, lens[b] - lp * 16)
                 np.testing.assert_array_equal(kpn[table[b, lp], :, :n],
                                               pack_int4(qr[b, :, lp * 16:lp * 16 + n]))
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_random_rows_contract(seed):
+    """Seeded random 2-D inputs through quantize_rows_into: row counts 1 to
+    ~40000 (every kernel form), channel counts 1 to 600, padded input row
+    strides (which decide between the 16-byte and the scalar kernels), packed
+    or unpacked bins into offset views of a larger pool; bins, scales and
+    zero-points bit-exact with the oracle and nothing outside the view
+    written."""
+    import torch
+    rng = np.random.RandomState(300 + seed)
+    rows = int(np.exp(rng.uniform(0, np.log(40000))))
+    C = int(rng.choice([int(rng.randint(1, 600)), 4 * int(rng.randint(1, 150))]))
+    pad = int(rng.choice([0, 0, 1, 3, 4, 8]))
+    packed = bool(rng.rand() < 0.5)
+    off = int(rng.choice([0, 1, 2, 4]))
+    kv = rng.randn(rows, C).astype(np.float32)
+    if rng.rand() < 0.3:
+        kv[:, rng.randint(C)] *= np.float32(20.0)          # an outlier channel
+    src = torch.zeros(rows, C + pad, device="cuda")
+    src[:, :C] = torch.from_numpy(kv).cuda()
+    nb = (C + 1) // 2 if packed else C
+    pool = torch.zeros(rows + 2, nb + off + 3, dtype=torch.uint8, device="cuda")
+    view = pool[1:rows + 1, off:off + nb]
+    s = torch.zeros(C, device="cuda")
+    z = torch.zeros(C, device="cuda")
+    _ops()._C.quantize_rows_into(src[:, :C], view, s, z, packed)
+    qr, sr, zr = quantize_int4_ref(kv)
+    got = pool.cpu().numpy()
+    want = pack_int4(qr) if packed else qr
+    np.testing.assert_array_equal(got[1:rows + 1, off:off + nb], want)
+    outside = got.copy()
+    outside[1:rows + 1, off:off + nb] = 0
+    assert not outside.any()
+    np.testing.assert_array_equal(s.cpu().numpy(), sr)
+    np.testing.assert_array_equal(z.cpu().numpy(), zr)
