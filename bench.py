@@ -46,8 +46,8 @@ The cpu_baseline leg times the NumPy oracle (the reference's page loop, one
 call per (sequence, head) stream, one BLAS thread) on this host's cores over
 the same workload and uses its output as the parity check of the GPU result.
 
-The HBM traffic of the decode kernel (and of the fake-quantization kernel)
-comes from two rocprofv3 --pmc child runs (FETCH_SIZE, then WRITE_SIZE), each
+The HBM traffic of the decode kernel (and of the grouped quantizer and the
+fake-quantization kernel) comes from two rocprofv3 --pmc child runs (FETCH_SIZE, then WRITE_SIZE), each
 calibrated by the same counter on a kernel that moves 256 MiB in that
 direction only (a sum for reads, a fill for writes); --no-pmc skips them (and
 must be given when this script itself runs under rocprofv3).
@@ -726,7 +726,8 @@ def pmc_child(args):
 def pmc_traffic(args):
     """HBM bytes per decode-kernel launch from FETCH_SIZE and WRITE_SIZE passes,
     each scaled by the same counter's reading for a kernel that moves 256 MiB
-    in that direction only; also the fake-quantization kernel's bytes."""
+    in that direction only; also the grouped quantizer's and the
+    fake-quantization kernel's bytes."""
     exe = shutil.which("rocprofv3")
     if exe is None:
         return None, "rocprofv3 not found"
@@ -759,13 +760,14 @@ def pmc_traffic(args):
         cal = values(lambda k: ("sum_functor" in k) if counter == "FETCH_SIZE"
                      else ("FillFunctor" in k))
         cpy = values(lambda k: "MulFunctor" in k)
+        qz = values(lambda k: "quantize_paged_kernel" in k)
         fq = {name: values(lambda k, t=tag: "fake_quant_kernel" in k and t in k)
               for name, tag in (("harness_window_f16", "F16Key"), ("decode_keys_f32", "F32Key"))}
         shutil.rmtree(d, ignore_errors=True)
         if not dec or not cal or not cpy:
             return None, f"no {counter} rows for the decode or calibration kernels"
         out[counter] = (median(dec), max(cal), {k: median(v) for k, v in fq.items() if v},
-                        max(cpy))
+                        max(cpy), median(qz) if qz else None)
     # Each calibration kernel moves 256 MiB in the counted direction: the
     # factor converts counter units to bytes. The copy's factors are reported
     # beside them (its reads can include line fills for its writes).
@@ -775,11 +777,15 @@ def pmc_traffic(args):
     fake = {name: {"fetch_bytes": out["FETCH_SIZE"][2][name] * ff,
                    "write_bytes": out["WRITE_SIZE"][2][name] * wf}
             for name in out["FETCH_SIZE"][2] if name in out["WRITE_SIZE"][2]}
+    quant = None
+    if out["FETCH_SIZE"][4] is not None and out["WRITE_SIZE"][4] is not None:
+        quant = {"fetch_bytes": out["FETCH_SIZE"][4] * ff,
+                 "write_bytes": out["WRITE_SIZE"][4] * wf}
     return {"fetch_bytes": out["FETCH_SIZE"][0] * ff, "write_bytes": out["WRITE_SIZE"][0] * wf,
             "fetch_factor_bytes_per_unit": ff, "write_factor_bytes_per_unit": wf,
             "copy_fetch_factor_bytes_per_unit": cal_bytes / out["FETCH_SIZE"][3],
             "copy_write_factor_bytes_per_unit": cal_bytes / out["WRITE_SIZE"][3],
-            "fake_quant": fake}, None
+            "fake_quant": fake, "quantizer": quant}, None
 
 
 def decode_kernel_label(w, value_dtype):
@@ -917,6 +923,11 @@ def main():
         traffic, err = pmc_traffic(args)
         if traffic is not None:
             fake = traffic.pop("fake_quant")
+            quant = traffic.pop("quantizer")
+            if quant is not None:
+                qt_bytes = round(quant["fetch_bytes"] + quant["write_bytes"])
+                line["quantizer_traffic"] = qt_bytes
+                line["quantizer_traffic_vs_algorithmic"] = round(qt_bytes / qbytes, 4)
             line["roofline"]["traffic"] = round(traffic["fetch_bytes"] + traffic["write_bytes"])
             line["roofline"]["traffic_detail"] = {k: round(v, 4) for k, v in traffic.items()}
             for name, t in fake.items():
