@@ -91,7 +91,11 @@ class INT4PagedKVCache:
     def write_block(self, block_id: int, k_block: np.ndarray, v_block: np.ndarray) -> None:
         """Quantize (one group over the block's rows), pack and store one block."""
         import torch
-        assert np.shape(k_block) == np.shape(v_block)
+        # The reference asserts equal shapes (src/vllm_integration.py:50); the
+        # same exception is raised explicitly so that it also holds under -O.
+        if np.shape(k_block) != np.shape(v_block):
+            raise AssertionError(f"k_block shape {np.shape(k_block)} != v_block shape "
+                                 f"{np.shape(v_block)}")
         rows, d = np.shape(k_block)
         if d != self.head_dim:
             raise ValueError(f"block has head_dim {d}, cache has {self.head_dim}")
@@ -206,6 +210,10 @@ class INT4PagedSequenceCache:
         self._free = list(range(num_pages - 1, -1, -1))
         self._pages = [[] for _ in range(max_seqs)]
         self._lens = np.zeros(max_seqs, dtype=np.int64)
+        self._mapped = np.zeros(max_seqs, dtype=np.int64)   # tokens the mapped pages hold
+        # Eager step() calls since the host lengths were last read from the
+        # device (replays of a captured step() are not counted).
+        self._unsynced_steps = 0
 
     # ---- page bookkeeping (host) -------------------------------------------
 
@@ -220,6 +228,18 @@ class INT4PagedSequenceCache:
             p = self._free.pop()
             updates.append((b, len(self._pages[b]), p))
             self._pages[b].append(p)
+            self._mapped[b] = len(self._pages[b]) * self.page_rows
+
+    def _grow_all(self, targets) -> None:
+        """Map pages so that sequence b holds n tokens, for (b, n) in targets.
+        Pages taken before a failure (out of pages, too long) are written to
+        the device page table too, so the host lists and the table agree."""
+        updates = []
+        try:
+            for b, n in targets:
+                self._grow(b, n, updates)
+        finally:
+            self._apply(updates)
 
     def _apply(self, updates: list) -> None:
         import torch
@@ -228,10 +248,18 @@ class INT4PagedSequenceCache:
         u = torch.tensor(updates, dtype=torch.int64).cuda()
         self.page_table[u[:, 0], u[:, 1]] = u[:, 2].to(torch.int32)
 
+    def _sync_if_stepped(self) -> None:
+        # step() advances the lengths on the device only; host-side page
+        # mapping must start from the device's lengths.
+        if self._unsynced_steps:
+            self.sync_lengths()
+
     def free(self, b: int) -> None:
         """Release sequence b's pages; its slot starts empty."""
+        self._sync_if_stepped()
         self._free.extend(reversed(self._pages[b]))
         self._pages[b] = []
+        self._mapped[b] = 0
         self._lens[b] = 0
         self.seq_lens[b] = 0
 
@@ -247,11 +275,10 @@ class INT4PagedSequenceCache:
             raise ValueError("k and v must be [batch, kv_heads, tokens, head_dim] of this cache")
         if B > self.max_seqs or len(lens) != B or (lens < 0).any() or (lens > T).any():
             raise ValueError("bad batch size or sequence lengths")
-        updates = []
+        self._sync_if_stepped()
         for b in range(B):
             self.free(b)
-            self._grow(b, int(lens[b]), updates)
-        self._apply(updates)
+        self._grow_all((b, int(lens[b])) for b in range(B))
         lens_t = torch.as_tensor(lens, dtype=torch.int32).cuda()
         self.seq_lens[:B] = lens_t
         self._lens[:B] = lens
@@ -278,10 +305,8 @@ class INT4PagedSequenceCache:
         B = k_new.shape[0]
         if B > self.max_seqs or tuple(k_new.shape) != (B, self.num_kv_heads, self.head_dim):
             raise ValueError("k_new must be [batch <= max_seqs, kv_heads, head_dim]")
-        updates = []
-        for b in range(B):
-            self._grow(b, int(self._lens[b]) + 1, updates)
-        self._apply(updates)
+        self._sync_if_stepped()
+        self._grow_all((b, int(self._lens[b]) + 1) for b in range(B))
         load_binding().append_paged(k_new, v_new.to(self.v_pages.dtype), self.k_stage[:B],
                                     self.k_pages, self.v_pages, self.k_scale[:B],
                                     self.k_zp[:B], self.page_table[:B], self.seq_lens[:B],
@@ -294,10 +319,8 @@ class INT4PagedSequenceCache:
     def reserve(self, batch: int, n_tokens: int) -> None:
         """Map the pages sequences 0..batch-1 need to grow by n_tokens, so that
         step() does no host work until they have."""
-        updates = []
-        for b in range(batch):
-            self._grow(b, int(self._lens[b]) + n_tokens, updates)
-        self._apply(updates)
+        self._sync_if_stepped()
+        self._grow_all((b, int(self._lens[b]) + n_tokens) for b in range(batch))
 
     def step(self, k_new, v_new, query, num_splits: int = 0):
         """One decode step on the device alone: append (k_new, v_new) [B,
@@ -306,19 +329,30 @@ class INT4PagedSequenceCache:
         returns [B, Hq, D] in the query's dtype.
         No host bookkeeping happens, so the call can be captured in a HIP
         graph and replayed: the pages must already be mapped (reserve), and
-        lengths() reflects the steps only after sync_lengths()."""
+        lengths() reflects the steps only after sync_lengths(); append(),
+        prefill(), reserve() and free() read the device lengths first.
+        An eager call whose token would fall outside the reserved pages raises
+        RuntimeError before anything is launched (the host knows the lengths up
+        to the eager steps since the last sync; replays are the caller's to
+        keep within the reservation)."""
         B = k_new.shape[0]
         if B > self.max_seqs or tuple(k_new.shape) != (B, self.num_kv_heads, self.head_dim):
             raise ValueError("k_new must be [batch <= max_seqs, kv_heads, head_dim]")
+        short = np.nonzero(self._lens[:B] + self._unsynced_steps + 1 > self._mapped[:B])[0]
+        if len(short):
+            raise RuntimeError(f"step() would write past the pages reserved for sequence "
+                               f"{int(short[0])}; call reserve() first")
         load_binding().append_paged(k_new, v_new, self.k_stage[:B], self.k_pages,
                                     self.v_pages, self.k_scale[:B], self.k_zp[:B],
                                     self.page_table[:B], self.seq_lens[:B], self.group_rows)
         self.seq_lens[:B] += 1
+        self._unsynced_steps += 1
         return self.decode(query, num_splits)
 
     def sync_lengths(self) -> None:
         """Refresh the host copy of the lengths from the device (after step())."""
         self._lens[:] = self.seq_lens.cpu().numpy()
+        self._unsynced_steps = 0
 
     # ---- reads -------------------------------------------------------------
 

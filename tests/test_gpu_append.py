@@ -137,6 +137,79 @@ def test_capacity_and_shapes_are_checked():
     assert c.lengths()[0] == 0 and c.memory_stats()["pages"] == 0
 
 
+def test_append_after_unsynced_steps():
+    """step() advances the lengths on the device only; an append() right after
+    (no sync_lengths()) must map pages from the device lengths. The lengths
+    after the steps end exactly on page (and group) boundaries, so the append
+    needs a page that the reservation did not map."""
+    import torch
+    B, H, D, group = 3, 2, 128, 128
+    lens0 = [13, 125, 301]
+    rng = np.random.RandomState(11)
+    cache = _cache(num_pages=64, num_kv_heads=H, head_dim=D, max_seqs=B, max_seq_len=400)
+    k0 = rng.randn(B, H, 320, D).astype(np.float32)
+    v0 = rng.randn(B, H, 320, D).astype(np.float32)
+    cache.prefill(torch.from_numpy(k0).cuda(), torch.from_numpy(v0).cuda(), lens0)
+    cache.reserve(B, 3)
+    new = [(rng.randn(B, H, D).astype(np.float32), rng.randn(B, H, D).astype(np.float32))
+           for _ in range(6)]
+    q = torch.from_numpy(rng.randn(B, H, D).astype(np.float32)).cuda()
+    for kn, vn in new[:3]:
+        cache.step(torch.from_numpy(kn).cuda(), torch.from_numpy(vn).cuda(), q)
+    for kn, vn in new[3:]:
+        cache.append(torch.from_numpy(kn).cuda(), torch.from_numpy(vn).cuda())
+    lens = [n + 6 for n in lens0]
+    assert list(cache.lengths()[:B]) == lens
+    streams = []
+    for b in range(B):
+        kb = np.concatenate([k0[b, :, :lens0[b]]] + [kn[b][:, None] for kn, _ in new], axis=1)
+        vb = np.concatenate([v0[b, :, :lens0[b]]] + [vn[b][:, None] for _, vn in new], axis=1)
+        streams.append((kb, vb))
+    _check_against_oracle(cache, streams, lens, group, "float32")
+
+
+def test_out_of_pages_keeps_the_page_table_consistent():
+    """An append that runs out of pages after mapping a page for an earlier
+    sequence must still write that page to the device table: the next append
+    of that sequence uses it without mapping it again."""
+    import torch
+    rng = np.random.RandomState(3)
+    c = _cache(num_pages=3, num_kv_heads=1, head_dim=64, max_seqs=2, max_seq_len=64,
+               group_rows=64)
+    k0 = rng.randn(2, 1, 16, 64).astype(np.float32)
+    v0 = rng.randn(2, 1, 16, 64).astype(np.float32)
+    c.prefill(torch.from_numpy(k0).cuda(), torch.from_numpy(v0).cuda(), [16, 16])
+    kn = [rng.randn(2, 1, 64).astype(np.float32) for _ in range(2)]
+    vn = [rng.randn(2, 1, 64).astype(np.float32) for _ in range(2)]
+    with pytest.raises(RuntimeError, match="out of pages"):
+        c.append(torch.from_numpy(kn[0]).cuda(), torch.from_numpy(vn[0]).cuda())
+    c.free(1)
+    c.append(torch.from_numpy(kn[1]).cuda(), torch.from_numpy(vn[1]).cuda())
+    streams = [(np.concatenate([k0[0], kn[1][0][:, None]], axis=1),
+                np.concatenate([v0[0], vn[1][0][:, None]], axis=1)),
+               (kn[1][1][:, None], vn[1][1][:, None])]
+    _check_against_oracle(c, streams, [17, 1], 64, "float32")
+
+
+def test_step_past_the_reservation_raises():
+    import torch
+    c = _cache(num_pages=4, num_kv_heads=1, head_dim=64, max_seqs=1, max_seq_len=64)
+    k = torch.zeros(1, 1, 16, 64, device="cuda")
+    c.prefill(k, k.clone(), [16])                # exactly one page mapped
+    kn = torch.zeros(1, 1, 64, device="cuda")
+    q = torch.zeros(1, 1, 64, device="cuda")
+    with pytest.raises(RuntimeError, match="reserve"):
+        c.step(kn, kn.clone(), q)
+    assert int(c.seq_lens[0]) == 16              # nothing was launched
+    c.reserve(1, 1)                              # maps the second page: 32 tokens
+    for _ in range(16):
+        c.step(kn, kn.clone(), q)
+    with pytest.raises(RuntimeError, match="reserve"):
+        c.step(kn, kn.clone(), q)                # both pages are full
+    c.sync_lengths()
+    assert c.lengths()[0] == 32 and int(c.seq_lens[0]) == 32
+
+
 @pytest.mark.parametrize("seed", range(24))
 def test_random_prefill_and_appends(seed):
     """Seeded random caches (head dims, page sizes 8-32, scale groups 64-256,
