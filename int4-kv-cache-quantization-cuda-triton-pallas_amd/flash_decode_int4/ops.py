@@ -40,7 +40,6 @@ HAS_EXTENSION = binding_available()
 #: True when the HIP extension is built and a GPU is visible.
 HAS_HIP = HAS_EXTENSION and gpu_available()
 HAS_CUDA = HAS_HIP
-_C = load_binding() if HAS_EXTENSION else None
 
 QUANTIZE_BACKENDS = ("hip", "cuda")
 ATTENTION_BACKENDS = ("hip", "cuda")
@@ -105,8 +104,9 @@ def prepare_quantize_int4_hip(kv) -> PreparedCall:
     if kv_t.dim() != 2:
         raise ValueError(f"the HIP quantizer takes a 2D [rows, channels] array, got shape "
                          f"{tuple(kv_t.shape)}")
+    C = load_binding()
     return PreparedCall(
-        run=lambda: _C.quantize_int4(kv_t),
+        run=lambda: C.quantize_int4(kv_t),
         sync=_sync,
         to_numpy=lambda out: tuple(t.cpu().numpy() for t in out),
     )
@@ -299,7 +299,7 @@ def backend_status() -> dict:
         "available_backends": ["hip", "cuda"] if HAS_HIP else [],
     }
     if HAS_EXTENSION:
-        status["abi_version"] = int(_C.abi_version())
+        status["abi_version"] = int(load_binding().abi_version())
     if status["gpu"]:
         status["device"] = torch.cuda.get_device_name(0)
     return status
