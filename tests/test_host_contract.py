@@ -203,6 +203,40 @@ class TestCABI:
             assert hasattr(lib, name), name
         assert set(declared) == set(capi.SIGNATURES), "ctypes table and header disagree"
 
+    def test_ctypes_prototypes_match_the_header(self):
+        """Parameter count and kind (pointer / int / int64 / size_t) and the
+        return kind of every ctypes prototype agree with include/fdi4.h."""
+        import ctypes
+        from flash_decode_int4 import capi
+        text = open(os.path.join(ROOT, "include", "fdi4.h")).read()
+        text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", " ", text)
+        protos = re.findall(r"([A-Za-z_][\w\s\*]*?)\b(fdi4_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;",
+                            text, flags=re.S)
+
+        def kind_c(decl):
+            decl = " ".join(decl.split())
+            if "*" in decl or "hipStream_t" in decl:
+                return "ptr"
+            base = decl.replace("const ", "").split()[0]
+            return {"int": "int", "int32_t": "int", "int64_t": "int64",
+                    "size_t": "size_t"}[base]
+
+        def kind_py(t):
+            if t in (ctypes.c_void_p, ctypes.c_char_p) or hasattr(t, "_type_") and \
+                    isinstance(getattr(t, "_type_"), type):
+                return "ptr"
+            return {ctypes.c_int: "int", ctypes.c_int32: "int", ctypes.c_int64: "int64",
+                    ctypes.c_size_t: "size_t"}[t]
+
+        assert {name for _, name, _ in protos} == set(capi.SIGNATURES)
+        for ret, name, params in protos:
+            params = " ".join(params.split())
+            c_args = [] if params in ("", "void") else [kind_c(p) for p in params.split(",")]
+            res, args = capi.SIGNATURES[name]
+            assert [kind_py(a) for a in args] == c_args, name
+            assert kind_py(res) == kind_c(ret.split("extern")[-1]), name
+
     def test_only_declared_symbols_are_exported(self):
         """Internal helpers stay out of the library's dynamic symbol table."""
         import shutil
