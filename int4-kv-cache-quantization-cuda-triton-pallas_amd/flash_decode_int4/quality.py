@@ -55,6 +55,14 @@ def _require_gpu_tensor(k) -> None:
         raise RuntimeError("k must be a GPU (cuda device) tensor; this build has no CPU path")
 
 
+def _byte_range(t):
+    """[first, last) bytes a tensor's elements span."""
+    if t.numel() == 0:
+        return t.data_ptr(), t.data_ptr()
+    span = sum((n - 1) * abs(st) for n, st in zip(t.shape, t.stride())) + 1
+    return t.data_ptr(), t.data_ptr() + span * t.element_size()
+
+
 def _aligned_rows(k):
     """k itself when its rows can be read as 16-byte vectors, else a contiguous copy."""
     esz = k.element_size()
@@ -105,6 +113,10 @@ def fake_quantize_keys(k, block_size: int = BLOCK_SIZE, rounding: str = "half_up
         out = torch.empty(k.shape, dtype=k.dtype, device=k.device)
     elif out.shape != k.shape or out.dtype != k.dtype:
         raise ValueError("out must have k's shape and dtype")
+    else:
+        (k0, k1), (o0, o1) = _byte_range(k), _byte_range(out)
+        if k0 < o1 and o0 < k1:
+            raise ValueError("out must not overlap k")
     if k.numel() == 0:
         return out
     load_binding().fake_quantize(_aligned_rows(k), out, block_size, ROUNDING_MODES[rounding],
@@ -148,7 +160,9 @@ def perplexity(model, input_ids, quantize_keys: bool, block_size: int = BLOCK_SI
 
     Windows of up to ``max_length`` tokens start every ``stride`` tokens; each
     scores only the tokens past the previous window's end. With
-    ``quantize_keys`` every window runs on a fresh key-quantizing cache.
+    ``quantize_keys`` every window runs on a fresh key-quantizing cache. A
+    window that scores no target (a last window of one fresh token) adds
+    nothing; the reference adds its undefined loss times zero, which is NaN.
 
     Returns {'ppl', 'tokens', 'windows'} plus, when quantizing, the hook
     evidence 'hook_calls' and 'max_abs_key_change'. Raises RuntimeError when
@@ -175,7 +189,8 @@ def perplexity(model, input_ids, quantize_keys: bool, block_size: int = BLOCK_SI
         with torch.no_grad():
             out = model(ids, **kwargs)
         scored = int((labels[:, 1:] != -100).sum())   # the loss averages shifted targets
-        nll += float(out.loss) * scored
+        if scored:
+            nll += float(out.loss) * scored
         scored_total += scored
         windows += 1
         done = end

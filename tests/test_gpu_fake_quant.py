@@ -168,6 +168,18 @@ def test_preallocated_out_and_empty():
     assert _fq(e).shape == e.shape
 
 
+def test_overlapping_out_is_rejected():
+    import torch
+    flat = torch.zeros(2 * 2 * 64 * 64, device="cuda")
+    k = flat[:2 * 64 * 64].view(1, 2, 64, 64)
+    with pytest.raises(ValueError, match="overlap"):
+        _fq(k, 64, out=k)
+    with pytest.raises(ValueError, match="overlap"):
+        _fq(k, 64, out=flat[64 * 64:3 * 64 * 64].view(1, 2, 64, 64))
+    out = flat[2 * 64 * 64:].view(1, 2, 64, 64)          # adjacent, not overlapping
+    assert _fq(k, 64, out=out) is out
+
+
 def test_argument_errors():
     import torch
     k = torch.zeros(1, 1, 8, 64, device="cuda")
@@ -328,6 +340,18 @@ class TestPerplexityHarness:
             direct = float(model(ids, labels=ids).loss)
         r = perplexity(model, ids, quantize_keys=False, max_length=2048, stride=1024)
         assert abs(np.log(r["ppl"]) - direct) < 1e-5
+
+    def test_window_with_nothing_to_score_adds_nothing(self):
+        """n = max_length + 1 with stride = max_length: the last window holds one
+        fresh token and no shifted target; the result is the first window's."""
+        from flash_decode_int4.quality import perplexity
+        model, ids = _tiny_llama(), _ids(257)
+        r = perplexity(model, ids, quantize_keys=True, max_length=256, stride=256)
+        first = perplexity(model, ids[:, :256], quantize_keys=True, max_length=256,
+                           stride=256)
+        assert r["windows"] == 2 and np.isfinite(r["ppl"])
+        assert r["tokens"] == first["tokens"] == 255
+        assert r["ppl"] == first["ppl"]
 
     def test_raises_when_attention_bypasses_the_cache(self):
         import torch
