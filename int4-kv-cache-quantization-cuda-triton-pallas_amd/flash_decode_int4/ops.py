@@ -41,6 +41,14 @@ HAS_EXTENSION = binding_available()
 HAS_HIP = HAS_EXTENSION and gpu_available()
 HAS_CUDA = HAS_HIP
 
+
+def __getattr__(name):
+    # ``ops._C`` is the torch binding, loaded on first use (so that a build in
+    # the same process after this module was imported is picked up).
+    if name == "_C":
+        return load_binding()
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
+
 QUANTIZE_BACKENDS = ("hip", "cuda")
 ATTENTION_BACKENDS = ("hip", "cuda")
 
