@@ -463,10 +463,6 @@ int carve_partials(void* workspace, size_t workspace_bytes, int batch, int hq, i
 
 }  // namespace
 
-extern "C" {
-
-}  // extern "C"
-
 namespace {
 
 int decode_paged_any(const void* query, int q_dtype, int batch, int num_q_heads,
