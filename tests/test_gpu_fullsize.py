@@ -2,7 +2,8 @@
 context-length sweep B8 H32 D128 at T = 512, 8192 and 32768, the last a
 4.3 GB value pool; B64 H32 D128 T4096, also a 4.3 GB pool whose byte offsets
 pass 2^32; ragged B32 up to 8192 tokens), through properties that do not
-depend on size plus sampled streams against the oracle:
+depend on size plus sampled streams against the oracle (float32 value pages;
+the anchor also with float16 and bfloat16 value pages):
 
 * the grouped quantizer is bit-exact on sampled (sequence, head) streams;
 * decoding is invariant, bit for bit, under a different physical page
@@ -26,10 +27,10 @@ def _ops():
     return ops
 
 
-def _build(name):
+def _build(name, value_dtype="float32"):
     import torch
     from flash_decode_int4.workloads import make_workload
-    w = make_workload(name, backend="torch", seed=2024)
+    w = make_workload(name, backend="torch", seed=2024, value_dtype=value_dtype)
     B, H, D = w["batch"], w["heads"], w["head_dim"]
     G = (w["max_tokens"] + 127) // 128
     dev = torch.device("cuda")
@@ -151,3 +152,23 @@ def test_split_counts_agree(built):
         got = _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
                                         st["sl"], num_splits=splits)
         assert (got - base).abs().max().item() < 5e-6, (name, splits)
+
+
+@pytest.mark.parametrize("value_dtype", ["float16", "bfloat16"])
+def test_16bit_values_at_the_anchor(value_dtype):
+    """B8 H32 D128 T2048 with 16-bit value pages: sampled streams of the full
+    decode against the oracle fed the same (widened) values."""
+    import torch
+    st = _build("anchor", value_dtype)
+    assert st["v"].dtype == getattr(torch, value_dtype)
+    out = _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
+                                    st["sl"])
+    assert out.dtype == torch.float32 and bool(out.isfinite().all())
+    for b, h in _streams(st, 6, seed=3):
+        args = _stream_problem(st, b, h)
+        o32, o64 = paged_decode_ref(*args)[0, 0], paged_decode_f64(*args)[0, 0]
+        got = out[b, h].cpu().numpy()
+        e32, eo = np.abs(got - o32).max(), np.abs(o32 - o64).max()
+        assert e32 <= max(TOL, 1.25 * eo), (value_dtype, b, h, e32, eo)
+    del st
+    torch.cuda.empty_cache()
