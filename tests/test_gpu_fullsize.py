@@ -3,7 +3,8 @@ context-length sweep B8 H32 D128 at T = 512, 8192 and 32768, the last a
 4.3 GB value pool; B64 H32 D128 T4096, also a 4.3 GB pool whose byte offsets
 pass 2^32; ragged B32 up to 8192 tokens), through properties that do not
 depend on size plus sampled streams against the oracle (float32 value pages;
-the anchor also with float16 and bfloat16 value pages):
+the anchor also with float16 and bfloat16 value pages; grouped query heads at
+B8 Hkv8 Hq32 T8192):
 
 * the grouped quantizer is bit-exact on sampled (sequence, head) streams;
 * decoding is invariant, bit for bit, under a different physical page
@@ -170,5 +171,31 @@ def test_16bit_values_at_the_anchor(value_dtype):
         got = out[b, h].cpu().numpy()
         e32, eo = np.abs(got - o32).max(), np.abs(o32 - o64).max()
         assert e32 <= max(TOL, 1.25 * eo), (value_dtype, b, h, e32, eo)
+    del st
+    torch.cuda.empty_cache()
+
+
+def test_grouped_query_heads_at_full_size():
+    """B8 Hkv8 Hq32 D128 T8192 (four q-heads per kv-head: the int8 matrix-core
+    kernel with splits and the merge): sampled (sequence, q-head) streams
+    against the oracle over the kv-head the q-head reads."""
+    import torch
+    st = _build("gqa")
+    w = st["w"]
+    hq, hkv = w["q_heads"], w["heads"]
+    assert st["q"].shape[1] == hq and hq == 4 * hkv
+    out = _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
+                                    st["sl"])
+    assert bool(out.isfinite().all())
+    rng = np.random.RandomState(4)
+    for _ in range(8):
+        b, qh = int(rng.randint(w["batch"])), int(rng.randint(hq))
+        q_, kp, vp, s_, z_, table, n, pr, grp = _stream_problem(st, b, qh // (hq // hkv))
+        q_ = st["q"][b:b + 1, qh:qh + 1].cpu().numpy()
+        args = (q_, kp, vp, s_, z_, table, n, pr, grp)
+        o32, o64 = paged_decode_ref(*args)[0, 0], paged_decode_f64(*args)[0, 0]
+        got = out[b, qh].cpu().numpy()
+        e32, eo = np.abs(got - o32).max(), np.abs(o32 - o64).max()
+        assert e32 <= max(TOL, 1.25 * eo), (b, qh, e32, eo)
     del st
     torch.cuda.empty_cache()
