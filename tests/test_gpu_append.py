@@ -168,6 +168,30 @@ def test_append_after_unsynced_steps():
     _check_against_oracle(cache, streams, lens, group, "float32")
 
 
+def test_append_at_the_anchor_size():
+    """B8 H32 D128, float32 values, prefill lengths around 2048 (on and next to
+    page and group edges), then two appends: every page and scale equals the
+    grouped quantizer over the whole sequences."""
+    import torch
+    B, H, D, group = 8, 32, 128, 128
+    lens0 = [2047, 2046, 2048, 2032, 1919, 1920, 2045, 1]
+    rng = np.random.RandomState(21)
+    k0 = rng.randn(B, H, 2048, D).astype(np.float32)
+    v0 = rng.randn(B, H, 2048, D).astype(np.float32)
+    cache = _cache(num_pages=B * 130, num_kv_heads=H, head_dim=D, max_seqs=B, max_seq_len=2064)
+    cache.prefill(torch.from_numpy(k0).cuda(), torch.from_numpy(v0).cuda(), lens0)
+    new = [(rng.randn(B, H, D).astype(np.float32), rng.randn(B, H, D).astype(np.float32))
+           for _ in range(2)]
+    for kn, vn in new:
+        cache.append(torch.from_numpy(kn).cuda(), torch.from_numpy(vn).cuda())
+    streams = []
+    for b in range(B):
+        kb = np.concatenate([k0[b, :, :lens0[b]]] + [kn[b][:, None] for kn, _ in new], axis=1)
+        vb = np.concatenate([v0[b, :, :lens0[b]]] + [vn[b][:, None] for _, vn in new], axis=1)
+        streams.append((kb, vb))
+    _check_against_oracle(cache, streams, [n + 2 for n in lens0], group, "float32")
+
+
 def test_out_of_pages_keeps_the_page_table_consistent():
     """An append that runs out of pages after mapping a page for an earlier
     sequence must still write that page to the device table: the next append
