@@ -1,6 +1,6 @@
 """GPU parity of the fused INT4 decode against the oracle.
 
-Tolerance (the north star's): max |HIP - oracle| <= 1e-5 on identical seeded
+Tolerance: max |HIP - oracle| <= 1e-5 on identical seeded
 inputs, where the oracle is the float32 page loop. The HIP kernel computes
 logits in float64, so it sits closer to the float64 arbiter than the float32
 oracle does; every test also checks the arbiter, and at sizes where the

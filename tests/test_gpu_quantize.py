@@ -1,5 +1,5 @@
 """GPU parity of the HIP quantizers against the oracle: bit-exact bins, packed
-bytes, scales and zero-points (the north star's bar; the reference itself
+bytes, scales and zero-points (the bar this path is held to; the reference itself
 held its CUDA/Triton quantizers only to "<= 1 bin on < 1%")."""
 
 import numpy as np
