@@ -142,7 +142,7 @@ def time_reference_config(steps, warmup):
     D128 queries all attending one shared stream of 8 pages x 256 rows
     (2048 tokens), each page one scale group with unpacked INT4 keys and fp32
     values (reference benchmarks/bench_three_backend.py:113-129, src/ops.py
-    :176-253). Keys are quantized with this build's quantize_int4; run() of
+    :176-253). Keys are quantized with the package's quantize_int4; run() of
     prepare_flash_decode_hip is timed (inputs staged in HBM once)."""
     import numpy as np
     import torch
@@ -807,7 +807,7 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build measures one GPU (the decode path shards by sequence "
+        print(f"bench.py measures one GPU (the decode path shards by sequence "
               f"and head with no exchange); --gpus {args.gpus} / WORLD_SIZE {world} is not "
               f"supported", file=sys.stderr)
         sys.exit(2)

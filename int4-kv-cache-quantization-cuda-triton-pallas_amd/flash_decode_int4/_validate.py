@@ -3,7 +3,7 @@
 Same contract and message substrings as the reference's
 src/_validate.py:11-64 ("query must be", "same length", "key page",
 "value page", "scale/zero-point", "entries", "outside"), so malformed input
-raises the same ValueError on this build as on the reference. The decode
+raises the same ValueError here as on the reference. The decode
 kernel additionally clamps every page length to [0, page_rows] and every
 page-table entry to the pool, so a malformed call that bypasses this check
 cannot read outside its buffers.

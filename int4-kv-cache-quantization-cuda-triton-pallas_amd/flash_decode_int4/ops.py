@@ -49,6 +49,7 @@ def __getattr__(name):
         return load_binding()
     raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
 
+
 QUANTIZE_BACKENDS = ("hip", "cuda")
 ATTENTION_BACKENDS = ("hip", "cuda")
 
@@ -77,7 +78,7 @@ def _validate_backend(backend: Optional[str], supported: tuple, op: str) -> None
             f"part of this package; supported backends for {op}: {supported}")
     if backend in ("triton", "pallas"):
         raise ValueError(
-            f"no {backend} kernels exist in this build (HIP only); supported backends for "
+            f"no {backend} kernels exist in this package (HIP only); supported backends for "
             f"{op}: {supported}")
     raise ValueError(f"unknown backend {backend!r} for {op}; supported: {supported}")
 
@@ -85,7 +86,7 @@ def _validate_backend(backend: Optional[str], supported: tuple, op: str) -> None
 def _require_device(use_cuda: Optional[bool]) -> None:
     if use_cuda is False:
         raise RuntimeError(
-            "use_cuda=False asks for a CPU implementation; this build has none (the kernels "
+            "use_cuda=False asks for a CPU implementation; this package has none (the kernels "
             "run on the GPU only)")
     if not HAS_EXTENSION:
         load_binding()  # raises with the reason

@@ -50,9 +50,9 @@ def _require_gpu_tensor(k) -> None:
     load_binding()  # raises with the reason when the extension is missing
     if not gpu_available():
         raise RuntimeError("fake_quantize_keys needs a visible GPU (torch.cuda.is_available() "
-                           "is False); this build has no CPU path")
+                           "is False); this package has no CPU path")
     if not k.is_cuda:
-        raise RuntimeError("k must be a GPU (cuda device) tensor; this build has no CPU path")
+        raise RuntimeError("k must be a GPU (cuda device) tensor; this package has no CPU path")
 
 
 def _byte_range(t):

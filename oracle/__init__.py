@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY. This package restates, in this project's own NumPy
 and C code, the reference's CPU algorithm so that the HIP kernels can be
 checked against it. Nothing in the product package
 (``flash_decode_int4``) imports it. The only permitted callers are ``tests/``,
-``__graft_entry__.smoke()`` (as the checker) and the ``cpu_baseline`` leg of
+``__graft_entry__.smoke()`` (to verify the GPU result) and the ``cpu_baseline`` leg of
 ``bench.py`` (as the timed CPU baseline). It is never the thing measured on
 the GPU and never a fallback.
 

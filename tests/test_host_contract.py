@@ -90,7 +90,7 @@ class TestAttentionInputContract:
 
 class TestBackendHonesty:
     """reference tests/test_ops_dispatch.py:90-139: a named backend is delivered or
-    refused, never substituted; this build has no CPU implementation."""
+    refused, never substituted; the package has no CPU implementation."""
 
     def test_unknown_backend(self):
         with pytest.raises(ValueError, match="unknown backend"):
@@ -99,7 +99,7 @@ class TestBackendHonesty:
             ops.quantize_int4(np.zeros((4, 4), np.float32), backend="nonsense")
 
     @pytest.mark.parametrize("name", ["reference", "triton", "pallas"])
-    def test_backends_not_in_this_build_are_refused(self, name):
+    def test_backends_not_in_this_package_are_refused(self, name):
         with pytest.raises(ValueError):
             ops.flash_decode(*_paged_problem(), backend=name)
         with pytest.raises(ValueError):
