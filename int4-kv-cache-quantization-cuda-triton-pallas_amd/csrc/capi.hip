@@ -136,6 +136,8 @@ int check_cache(const fdi4_paged_cache* c, bool need_values) {
       c->num_pages < 1)
     return hipErrorInvalidValue;
   if (c->s_page_stride != 0 && c->pages_per_group != 1) return hipErrorInvalidValue;
+  // Token positions within a sequence are 32-bit in the kernels.
+  if ((int64_t)c->max_pages * c->page_rows > INT32_MAX) return hipErrorInvalidValue;
   const int kbl = c->head_dim == 64 ? 8 : 16;  // bytes a lane loads from a key row
   if (!aligned(c->k_pages, kbl) || c->k_page_stride % kbl || c->k_head_stride % kbl ||
       c->k_row_stride % kbl || c->k_row_stride < c->head_dim / 2)

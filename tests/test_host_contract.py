@@ -301,6 +301,15 @@ class TestCABI:
         big.v_row_stride = 1 << 25
         assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
                                      None, 0, None) == bad
+        # Sequences of 2^32 token positions (max_pages x page_rows) do not fit
+        # the kernels' 32-bit token indices.
+        big.v_row_stride = 128
+        big.page_rows, big.max_pages, big.pages_per_group = 32, 1 << 27, 4
+        big.page_table, big.pt_batch_stride = 256, 1 << 27
+        assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
+                                     None, 0, None) == bad
+        assert lib.fdi4_append_paged(q, 128, 128, q, 128, 128, 1, q, 1 << 14, 1 << 14, 128,
+                                     128, ctypes.byref(big), None) == bad
 
     def test_typed_decode_rejects_unknown_element_types(self):
         """fdi4_decode_paged_ex: query and output types are 0, 1, 2 (float32,
