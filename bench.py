@@ -793,12 +793,14 @@ def pmc_traffic(args):
 def decode_kernel_label(w, value_dtype):
     """The decode kernel the library's planner picks for this workload: the
     per-head kernel for one q-head per kv-head, the int8 matrix-core kernel
-    for grouped heads at head_dim 64 / 128 (unless FDI4_DECODE_MFMA=0), the
-    vector grouped kernel otherwise."""
+    for grouped heads at head_dim 64 / 128 (unless the decode_vector_only
+    override is set), the vector grouped kernel otherwise."""
+    from flash_decode_int4 import capi
     d, rep = w["head_dim"], w["q_heads"] // w["heads"]
     if rep == 1:
         return f"decode_kernel<D={d}, {value_dtype} values>"
-    kind = ("decode_mfma_kernel" if d in (64, 128) and os.environ.get("FDI4_DECODE_MFMA") != "0"
+    vector_only = capi.load().fdi4_get_tuning(capi.TUNE["decode_vector_only"]) == 1
+    kind = ("decode_mfma_kernel" if d in (64, 128) and not vector_only
             else "decode_gqa_kernel")
     return f"{kind}<D={d}, {value_dtype} values, {rep} q-heads per kv-head>"
 

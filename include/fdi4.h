@@ -78,6 +78,40 @@ typedef struct fdi4_paged_cache {
   int32_t num_pages;  /* physical pages in the pool */
 } fdi4_paged_cache;
 
+/* Launch-shape overrides, for measurement and tests; production callers
+ * need none of them. The library reads no environment variables: the
+ * automatic choices below apply unless a caller sets a knob here. Settings
+ * are process-wide and take effect for calls made after fdi4_set_tuning
+ * returns; value 0 restores the automatic choice.
+ *
+ *   FDI4_TUNE_DECODE_VECTOR_ONLY   1: grouped-head decodes at head_dim 64/128
+ *                                  run on the vector kernels instead of the
+ *                                  int8 matrix-core kernel
+ *   FDI4_TUNE_DECODE_WAVES         4 or 8 wave64s per decode workgroup
+ *   FDI4_TUNE_DECODE_HEADS_PER_WG  cap on q-heads per decode workgroup: 1
+ *                                  (per-head kernel), 2, 4 or 8
+ *   FDI4_TUNE_DECODE_TARGET_WAVES  resident waves the split count aims for
+ *                                  (1 .. 1<<20)
+ *   FDI4_TUNE_FAKE_QUANT_SPLIT     channel slices per key row of
+ *                                  fdi4_fake_quantize (1 .. 512)
+ */
+enum fdi4_tuning_knob {
+  FDI4_TUNE_DECODE_VECTOR_ONLY = 0,
+  FDI4_TUNE_DECODE_WAVES = 1,
+  FDI4_TUNE_DECODE_HEADS_PER_WG = 2,
+  FDI4_TUNE_DECODE_TARGET_WAVES = 3,
+  FDI4_TUNE_FAKE_QUANT_SPLIT = 4,
+  FDI4_TUNE_COUNT = 5
+};
+
+/* Set a knob (hipErrorInvalidValue for an unknown knob or a value outside
+ * its range; the setting is then unchanged). No counterpart in the
+ * reference, whose launch shapes are fixed. */
+int fdi4_set_tuning(int knob, int value);
+
+/* Current value of a knob (0 = automatic; -1 for an unknown knob). */
+int fdi4_get_tuning(int knob);
+
 /* ABI version of the loaded library (FDI4_ABI_VERSION). */
 int fdi4_abi_version(void);
 

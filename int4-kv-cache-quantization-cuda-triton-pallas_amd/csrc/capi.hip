@@ -10,6 +10,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 
@@ -25,7 +26,7 @@ using fdi4::QuantPagedArgs;
 // smallest that gives about kTargetWaves resident waves (8 per CU on 256 CUs,
 // the occupancy the decode kernel's ~200 VGPRs allow), so that with enough
 // (sequence, head) streams no split -- and no merge kernel -- is needed.
-// FDI4_DECODE_WAVES and FDI4_DECODE_TARGET_WAVES override the choice (tuning).
+// FDI4_TUNE_DECODE_WAVES and FDI4_TUNE_DECODE_TARGET_WAVES override the choice.
 constexpr int kTargetWaves = 2048;
 constexpr int kMinChunksPerWave = 4;
 constexpr size_t kAlign = 256;
@@ -42,11 +43,20 @@ int chunks_per_seq(const fdi4_paged_cache* c) {
   return c->max_pages * ceil_div(c->page_rows, 16);
 }
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  if (!v || !*v) return dflt;
-  const int x = atoi(v);
-  return x > 0 ? x : dflt;
+// Launch-shape overrides set through fdi4_set_tuning (0 = automatic). Atomic
+// so that a setting made on one thread is seen, whole, by launches on another.
+std::atomic<int> g_tuning[FDI4_TUNE_COUNT];
+
+bool tuning_value_ok(int knob, int v) {
+  if (v == 0) return true;
+  switch (knob) {
+    case FDI4_TUNE_DECODE_VECTOR_ONLY: return v == 1;
+    case FDI4_TUNE_DECODE_WAVES: return v == 4 || v == 8;
+    case FDI4_TUNE_DECODE_HEADS_PER_WG: return v == 1 || v == 2 || v == 4 || v == 8;
+    case FDI4_TUNE_DECODE_TARGET_WAVES: return v >= 1 && v <= (1 << 20);
+    case FDI4_TUNE_FAKE_QUANT_SPLIT: return v >= 1 && v <= 512;
+    default: return false;
+  }
 }
 
 // Eight waves as soon as each gets kMinChunksPerWave chunks: more waves per
@@ -54,7 +64,7 @@ int env_int(const char* name, int dflt) {
 // T512, 8 waves and one split take 16.5 us against 19.2 us for 4 waves, two
 // splits and the merge).
 int pick_waves(int chunks) {
-  const int w = env_int("FDI4_DECODE_WAVES", 0);
+  const int w = g_tuning[FDI4_TUNE_DECODE_WAVES].load(std::memory_order_relaxed);
   if (w == 4 || w == 8) return w;
   return chunks >= 8 * kMinChunksPerWave ? 8 : 4;
 }
@@ -62,10 +72,15 @@ int pick_waves(int chunks) {
 // Query heads one decode workgroup serves (heads of one kv-head, so their
 // keys and values are read once for all of them): the largest of 8, 4, 2 that
 // divides Hq/Hkv within what registers and LDS allow (8 at D=64, 4 at D=128
-// and 256); 1 runs the per-head kernel. FDI4_DECODE_HEADS_PER_WG caps the
-// choice (tuning; 1 disables grouping).
+// and 256); 1 runs the per-head kernel. FDI4_TUNE_DECODE_HEADS_PER_WG caps the
+// choice (1 disables grouping).
+int heads_per_wg_cap() {
+  const int c = g_tuning[FDI4_TUNE_DECODE_HEADS_PER_WG].load(std::memory_order_relaxed);
+  return c > 0 ? c : 8;
+}
+
 int pick_heads_per_wg(int d, int hq_per_kv) {
-  const int cap = std::min(env_int("FDI4_DECODE_HEADS_PER_WG", 8), d == 64 ? 8 : 4);
+  const int cap = std::min(heads_per_wg_cap(), d == 64 ? 8 : 4);
   for (int hg : {8, 4, 2})
     if (hg <= cap && hq_per_kv % hg == 0) return hg;
   return 1;
@@ -75,12 +90,11 @@ int pick_heads_per_wg(int d, int hq_per_kv) {
 // int8 matrix-core kernel (2, 4 or 8 heads per workgroup, 8 only at D=64;
 // B8 Hkv8 Hq32 T8192: 61 us against 75 us for the vector grouped kernel);
 // with one head per kv-head the vector per-head kernel, which is faster there
-// (anchor 51.9 against 54.2 us). FDI4_DECODE_MFMA=0 selects the vector
-// kernels throughout (tuning and A/B measurement).
+// (anchor 51.9 against 54.2 us). FDI4_TUNE_DECODE_VECTOR_ONLY selects the
+// vector kernels throughout (A/B measurement).
 bool use_mfma(int d) {
-  const char* v = getenv("FDI4_DECODE_MFMA");
-  const bool on = !(v && v[0] == '0');
-  return on && (d == 64 || d == 128);
+  const bool off = g_tuning[FDI4_TUNE_DECODE_VECTOR_ONLY].load(std::memory_order_relaxed) == 1;
+  return !off && (d == 64 || d == 128);
 }
 
 // Up to eight heads per workgroup (at D=128: 248 VGPRs with float32 values,
@@ -88,7 +102,7 @@ bool use_mfma(int d) {
 int pick_heads_per_wg_mfma(int d, int v_dtype, int hq_per_kv) {
   (void)d;
   (void)v_dtype;
-  const int cap = std::min(env_int("FDI4_DECODE_HEADS_PER_WG", 8), 8);
+  const int cap = heads_per_wg_cap();
   for (int hg : {8, 4, 2})
     if (hg <= cap && hq_per_kv % hg == 0) return hg;
   return 1;
@@ -115,7 +129,8 @@ DecodePlan plan_decode(int batch, int hq, int hq_per_kv, int d, int v_dtype, int
     p.splits = 1;
     return p;
   }
-  const int64_t target = env_int("FDI4_DECODE_TARGET_WAVES", kTargetWaves);
+  const int tw = g_tuning[FDI4_TUNE_DECODE_TARGET_WAVES].load(std::memory_order_relaxed);
+  const int64_t target = tw > 0 ? tw : kTargetWaves;
   const int64_t per_split = (int64_t)batch * (hq / p.heads_per_wg) * p.waves;
   const int s = (int)((target + per_split - 1) / per_split);
   const int smax = std::max(1, chunks / (p.waves * kMinChunksPerWave));
@@ -196,7 +211,24 @@ hipError_t temp_alloc(void** ptr, size_t bytes, hipStream_t stream) {
 
 }  // namespace
 
+int fdi4::tuning(int knob) {
+  return (knob >= 0 && knob < FDI4_TUNE_COUNT) ? g_tuning[knob].load(std::memory_order_relaxed)
+                                               : 0;
+}
+
 extern "C" {
+
+int fdi4_set_tuning(int knob, int value) {
+  if (knob < 0 || knob >= FDI4_TUNE_COUNT || !tuning_value_ok(knob, value))
+    return hipErrorInvalidValue;
+  g_tuning[knob].store(value, std::memory_order_relaxed);
+  return hipSuccess;
+}
+
+int fdi4_get_tuning(int knob) {
+  if (knob < 0 || knob >= FDI4_TUNE_COUNT) return -1;
+  return g_tuning[knob].load(std::memory_order_relaxed);
+}
 
 int fdi4_abi_version(void) { return FDI4_ABI_VERSION; }
 

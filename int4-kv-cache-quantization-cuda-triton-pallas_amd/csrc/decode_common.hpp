@@ -104,10 +104,34 @@ __device__ __forceinline__ ChunkMeta chunk_meta(const DecodeArgs& a, int b, int 
   return m;
 }
 
-// Valid rows of sequence b (every sequence spans max_pages pages when no
-// lengths are given).
+// Valid rows of sequence b, clamped to the max_pages * page_rows the cache
+// holds (the host checks that this product fits in 32 bits), so no count
+// derived from a length overflows; every sequence spans max_pages pages when
+// no lengths are given.
 __device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
-  return a.seq_lens ? max(a.seq_lens[b], 0) : a.max_pages * a.page_rows;
+  const int cap = a.max_pages * a.page_rows;
+  return a.seq_lens ? min(max(a.seq_lens[b], 0), cap) : cap;
+}
+
+// Logical pages holding the first T rows (T <= max_pages * page_rows).
+__device__ __forceinline__ int pages_of(const DecodeArgs& a, int T) {
+  return T / a.page_rows + (T % a.page_rows != 0);
+}
+
+// Chunk range [c0, c1) of wave w of `waves` over the chunks [begin, end) of a
+// split: every wave gets span / waves chunks and the last span % waves waves
+// one more. A sequence's last chunk -- the partial one when the length is not
+// a multiple of 16 rows -- thus lands on a wave whose other chunks are full,
+// and the full chunks are spread evenly: at 129 chunks over 8 waves, seven
+// waves stream 16 chunks and one streams 16 plus the partial one (rounding the
+// share up instead would give seven waves 17 full chunks and one wave 10).
+__device__ __forceinline__ void wave_chunks(int begin, int end, int w, int waves, int& c0,
+                                            int& c1) {
+  const int span = max(end - begin, 0);
+  const int base = span / waves, rem = span - base * waves;
+  const int first_long = waves - rem;
+  c0 = begin + w * base + max(w - first_long, 0);
+  c1 = c0 + base + (w >= first_long ? 1 : 0);
 }
 
 // exp(x) for x <= ~0 in double: the exponent x*log2(e) is formed in double,

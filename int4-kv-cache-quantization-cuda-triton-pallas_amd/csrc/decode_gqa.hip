@@ -96,21 +96,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gqa_kernel(DecodeArgs a) {
   __shared__ float l_s[WAVES][HG];
 
   const int cpp = (a.page_rows + 15) >> 4;
-  int T, n_lp;
-  if (a.seq_lens) {
-    T = max(a.seq_lens[b], 0);
-    n_lp = min((T + a.page_rows - 1) / a.page_rows, a.max_pages);
-  } else {
-    n_lp = a.max_pages;
-    T = n_lp * a.page_rows;
-  }
-  const int n_chunks = n_lp * cpp;
+  const int T = seq_len_of(a, b);
+  const int n_chunks = pages_of(a, T) * cpp;
   const int c_begin = split * a.chunks_per_split;
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
-  const int span = max(c_end - c_begin, 0);
-  const int per_wave = (span + WAVES - 1) / WAVES;
-  const int wc0 = c_begin + w * per_wave;
-  const int wc1 = min(wc0 + per_wave, c_end);
+  int wc0, wc1;
+  wave_chunks(c_begin, c_end, w, WAVES, wc0, wc1);
 
   double m_run[HG];
   float l_lane[HG];

@@ -91,14 +91,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
 
   const int cpp = (a.page_rows + 15) >> 4;
   const int T = seq_len_of(a, b);
-  const int n_lp = min((T + a.page_rows - 1) / a.page_rows, a.max_pages);
-  const int n_chunks = n_lp * cpp;
+  const int n_chunks = pages_of(a, T) * cpp;
   const int c_begin = split * a.chunks_per_split;
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
-  const int span = max(c_end - c_begin, 0);
-  const int per_wave = (span + WAVES - 1) / WAVES;
-  const int wc0 = c_begin + w * per_wave;
-  const int wc1 = min(wc0 + per_wave, c_end);
+  int wc0, wc1;
+  wave_chunks(c_begin, c_end, w, WAVES, wc0, wc1);
 
   // Softmax state of head n16 (meaningful on head lanes).
   double m_run = -INFINITY;

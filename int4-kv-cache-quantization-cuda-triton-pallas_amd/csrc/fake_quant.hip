@@ -264,10 +264,6 @@ hipError_t launch_rounding(const FakeQuantArgs& a, int rounding, dim3 grid, hipS
                                         : launch_typed<KT, FDI4_ROUND_HALF_EVEN>(a, grid, st);
 }
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v && *v ? atoi(v) : dflt;
-}
 
 }  // namespace
 
@@ -286,9 +282,10 @@ hipError_t launch_fake_quant(const FakeQuantArgs& args, int key_dtype, int round
   // head_dim 64 and 128 (8 x 32 x 2048 x 128 float32 in 128-row blocks:
   // 93 us against 103 us for whole rows and 96 us for 256-byte slices; a
   // Llama-2-7B window, 32 x 2048 x 128 float16 in 256-row blocks: 11.4 us
-  // against 15.2 and 12.2 us). FDI4_FAKE_QUANT_SPLIT overrides (tuning).
+  // against 15.2 and 12.2 us). FDI4_TUNE_FAKE_QUANT_SPLIT overrides it.
   const int row_bytes = a.head_dim * esz;
-  int split = env_int("FDI4_FAKE_QUANT_SPLIT", row_bytes >= 128 ? row_bytes / 128 : 1);
+  const int forced = tuning(FDI4_TUNE_FAKE_QUANT_SPLIT);
+  int split = forced > 0 ? forced : (row_bytes >= 128 ? row_bytes / 128 : 1);
   while (split > 1 && (a.head_dim % split || (a.head_dim / split * esz) % 16 ||
                        nblk * split > INT32_MAX))
     --split;

@@ -91,6 +91,9 @@ struct FakeQuantArgs {
   int nsplit, cw, vpr, rpp;
 };
 
+// Value of a launch-shape override (fdi4_set_tuning; 0 = automatic).
+int tuning(int knob);
+
 hipError_t launch_quantize_rows(const float* kv, int64_t rows, int C, int64_t stride, uint8_t* q,
                                 int64_t q_stride, bool packed, float* scale_out, float* zp_out,
                                 void* ws, hipStream_t st);

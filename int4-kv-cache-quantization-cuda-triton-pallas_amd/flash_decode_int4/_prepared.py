@@ -16,26 +16,30 @@ from dataclasses import dataclass
 from typing import Any, Callable, Optional
 
 
-def _no_sync(_out: Any) -> None:
-    return None
+def _skip_wait(result: Any) -> None:
+    """Default wait step: the result needs no device synchronization."""
+    del result
 
 
-def _identity(out: Any) -> Any:
-    return out
+def _as_is(result: Any) -> Any:
+    """Default host step: hand the result back unchanged."""
+    return result
 
 
 @dataclass
 class PreparedCall:
-    #: Enqueue the computation on staged inputs; returns device outputs.
+    """``run`` enqueues the staged launch and returns its device result;
+    ``sync`` waits on the stream that result was produced on; ``to_numpy``
+    moves that result to host memory for checking (never timed);
+    ``lowered_text`` is a hook for backends that expose the compiled program
+    (None here: the kernels are prebuilt HIP code objects)."""
+
     run: Callable[[], Any]
-    #: Block until the outputs of run() are complete.
-    sync: Callable[[Any], None] = _no_sync
-    #: Copy run()'s outputs to host NumPy (kept out of any timed region).
-    to_numpy: Callable[[Any], Any] = _identity
-    #: Text of the lowered program where that is meaningful (unused here).
+    sync: Callable[[Any], None] = _skip_wait
+    to_numpy: Callable[[Any], Any] = _as_is
     lowered_text: Optional[Callable[[], str]] = None
 
     def __call__(self) -> Any:
-        out = self.run()
-        self.sync(out)
-        return self.to_numpy(out)
+        result = self.run()
+        self.sync(result)
+        return self.to_numpy(result)

@@ -19,6 +19,9 @@ V_BF16 = 2
 K_F32, K_F16, K_BF16 = 0, 1, 2
 ROUND_HALF_UP, ROUND_HALF_EVEN = 0, 1
 SCALE_DIVIDE, SCALE_RECIPROCAL = 0, 1
+#: fdi4_tuning_knob codes (launch-shape overrides for measurement and tests).
+TUNE = {"decode_vector_only": 0, "decode_waves": 1, "decode_heads_per_wg": 2,
+        "decode_target_waves": 3, "fake_quant_split": 4}
 
 
 class PagedCache(ctypes.Structure):
@@ -49,6 +52,8 @@ class PagedCache(ctypes.Structure):
 
 #: name -> (restype, argtypes); the complete exported surface of include/fdi4.h.
 SIGNATURES = {
+    "fdi4_set_tuning": (c_int, [c_int, c_int]),
+    "fdi4_get_tuning": (c_int, [c_int]),
     "fdi4_abi_version": (c_int, []),
     "fdi4_error_string": (ctypes.c_char_p, [c_int]),
     "fdi4_quantize_int4": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p,
@@ -113,3 +118,34 @@ def check(rc: int, what: str = "fdi4 call") -> None:
     if rc != 0:
         msg = load().fdi4_error_string(rc)
         raise RuntimeError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")
+
+
+class tuning:
+    """Context manager that sets launch-shape overrides (``fdi4_set_tuning``)
+    for the calls made inside it and restores the previous values on exit:
+
+        with capi.tuning(decode_vector_only=1):
+            out = ops.flash_decode_paged(...)
+
+    Process-wide: calls made meanwhile on other threads see the settings too.
+    """
+
+    def __init__(self, **knobs):
+        unknown = set(knobs) - set(TUNE)
+        if unknown:
+            raise ValueError(f"unknown tuning knobs {sorted(unknown)}; known: {sorted(TUNE)}")
+        self._knobs = {TUNE[k]: int(v) for k, v in knobs.items()}
+        self._saved = {}
+
+    def __enter__(self):
+        lib = load()
+        for knob, value in self._knobs.items():
+            self._saved[knob] = lib.fdi4_get_tuning(knob)
+            check(lib.fdi4_set_tuning(knob, value), f"fdi4_set_tuning({knob}, {value})")
+        return self
+
+    def __exit__(self, *exc):
+        lib = load()
+        for knob, value in self._saved.items():
+            lib.fdi4_set_tuning(knob, value)
+        return False

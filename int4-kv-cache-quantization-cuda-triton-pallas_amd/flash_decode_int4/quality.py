@@ -1,16 +1,17 @@
-"""On-device INT4 fake quantization of keys, for quality (perplexity) studies.
+"""On-device INT4 fake quantization of keys, for quality studies.
 
-Drop-in for the key-quantizing pieces of the reference's perplexity harness
-(scripts/validate_llama.py:52, 126-249): ``BLOCK_SIZE``,
-``fake_quantize_keys``, ``make_key_quantizing_cache`` and ``perplexity``. The
-quantize-dequantize runs in one HIP kernel (``fdi4_fake_quantize``: one read
-and one write of the keys) instead of the reference's chain of torch
-operations (pad, amin, amax, divide, floor, clamp, multiply, add, cast), with
-the same float32 arithmetic.
+Device form of the key quantize-dequantize of the reference's quality study
+(``fake_quantize_keys``, scripts/validate_llama.py:126-154, with its block
+size ``BLOCK_SIZE`` of :52). The quantize-dequantize runs in one HIP kernel
+(``fdi4_fake_quantize``: one read and one write of the keys) instead of the
+reference's chain of torch operations (pad, amin, amax, divide, floor,
+clamp, multiply, add, cast), with the same float32 arithmetic. The study's
+model driver (cache hook, sliding-window perplexity, weight and dataset
+loading) is not part of this package.
 
 Options beyond the reference's signature:
 
-``rounding``  "half_up" is the harness's rule (floor(t + 0.5), dq = q*scale +
+``rounding``  "half_up" is the study's rule (floor(t + 0.5), dq = q*scale +
               mn); "half_even" is the scheme the INT4 cache stores and the
               attention kernels dequantize (round half to even, dq = q*scale -
               zp*scale; reference src/quantize_int4_ref.py:139-158 per block),
@@ -28,8 +29,6 @@ CPU path (the call raises without the HIP extension or a GPU).
 """
 
 from typing import Optional
-
-import numpy as np
 
 from ._lib import gpu_available, load_binding
 
@@ -122,94 +121,3 @@ def fake_quantize_keys(k, block_size: int = BLOCK_SIZE, rounding: str = "half_up
     load_binding().fake_quantize(_aligned_rows(k), out, block_size, ROUNDING_MODES[rounding],
                                  SCALE_OPS[scale_op])
     return out
-
-
-def make_key_quantizing_cache(block_size: int, stats: dict, rounding: str = "half_up",
-                              scale_op: str = "divide"):
-    """A transformers DynamicCache whose update() returns INT4-quantized keys.
-
-    Attention attends over update()'s return value, so wrapping it on the
-    instance quantizes exactly the keys attention reads; the cache itself keeps
-    the full-precision keys. ``stats`` gains 'hook_calls' (times the hook
-    fired) and 'max_abs_key_change' (largest |kq - k| seen), the evidence that
-    a run measured something. reference: scripts/validate_llama.py:157-178.
-    """
-    from transformers import DynamicCache
-
-    stats.setdefault("hook_calls", 0)
-    stats.setdefault("max_abs_key_change", 0.0)
-    cache = DynamicCache()
-    original_update = cache.update
-
-    def update(key_states, value_states, layer_idx, *args, **kwargs):
-        k, v = original_update(key_states, value_states, layer_idx, *args, **kwargs)
-        kq = fake_quantize_keys(k, block_size, rounding, scale_op)
-        stats["hook_calls"] += 1
-        change = float((kq.float() - k.float()).abs().max()) if k.numel() else 0.0
-        stats["max_abs_key_change"] = max(stats["max_abs_key_change"], change)
-        return kq, v
-
-    cache.update = update
-    return cache
-
-
-def perplexity(model, input_ids, quantize_keys: bool, block_size: int = BLOCK_SIZE,
-               max_length: int = 2048, stride: int = 1024, rounding: str = "half_up",
-               scale_op: str = "divide") -> dict:
-    """Sliding-window perplexity, optionally with INT4 keys inside attention.
-
-    Windows of up to ``max_length`` tokens start every ``stride`` tokens; each
-    scores only the tokens past the previous window's end. With
-    ``quantize_keys`` every window runs on a fresh key-quantizing cache. A
-    window that scores no target (a last window of one fresh token) adds
-    nothing; the reference adds its undefined loss times zero, which is NaN.
-
-    Returns {'ppl', 'tokens', 'windows'} plus, when quantizing, the hook
-    evidence 'hook_calls' and 'max_abs_key_change'. Raises RuntimeError when
-    quantization was requested but the hook never fired (the model does not
-    read keys through Cache.update()) or left every key unchanged -- either
-    would report a full-precision number as an INT4 one.
-    reference: scripts/validate_llama.py:181-249.
-    """
-    import torch
-
-    n = input_ids.size(1)
-    stats = {"hook_calls": 0, "max_abs_key_change": 0.0}
-    nll, scored_total, windows, done = 0.0, 0, 0, 0
-    for begin in range(0, n, stride):
-        end = min(begin + max_length, n)
-        ids = input_ids[:, begin:end]
-        labels = ids.clone()
-        fresh = end - done                      # tokens not scored by an earlier window
-        labels[:, :-fresh] = -100
-        kwargs = {"labels": labels, "use_cache": True}
-        if quantize_keys:
-            kwargs["past_key_values"] = make_key_quantizing_cache(block_size, stats, rounding,
-                                                                  scale_op)
-        with torch.no_grad():
-            out = model(ids, **kwargs)
-        scored = int((labels[:, 1:] != -100).sum())   # the loss averages shifted targets
-        if scored:
-            nll += float(out.loss) * scored
-        scored_total += scored
-        windows += 1
-        done = end
-        if end == n:
-            break
-
-    if quantize_keys:
-        if stats["hook_calls"] == 0:
-            raise RuntimeError(
-                "INT4 key hook never fired: the model's attention does not read keys through "
-                "Cache.update(), so no quantization took place; refusing to report a "
-                "full-precision perplexity as an INT4 result.")
-        if stats["max_abs_key_change"] == 0.0:
-            raise RuntimeError(
-                "INT4 key hook fired but left every key unchanged; the measurement would be "
-                "indistinguishable from full precision.")
-
-    result = {"ppl": float(np.exp(nll / max(scored_total, 1))), "tokens": scored_total,
-              "windows": windows}
-    if quantize_keys:
-        result.update(stats)
-    return result

@@ -218,17 +218,22 @@ class INT4PagedSequenceCache:
     # ---- page bookkeeping (host) -------------------------------------------
 
     def _grow(self, b: int, n_tokens: int, updates: list) -> None:
+        """Map the pages sequence b needs to hold n_tokens, taking them from
+        the free list in one slice (the order successive pops would give)."""
         need = (n_tokens + self.page_rows - 1) // self.page_rows
         if need > self.max_pages_per_seq:
             raise ValueError(f"sequence {b} would hold {n_tokens} tokens; the cache holds "
                              f"{self.max_pages_per_seq * self.page_rows} per sequence")
-        while len(self._pages[b]) < need:
-            if not self._free:
-                raise RuntimeError("out of pages")
-            p = self._free.pop()
-            updates.append((b, len(self._pages[b]), p))
-            self._pages[b].append(p)
+        have = len(self._pages[b])
+        take = min(need - have, len(self._free))
+        if take > 0:
+            new = self._free[len(self._free) - take:][::-1]
+            del self._free[len(self._free) - take:]
+            updates.append((b, have, np.asarray(new, dtype=np.int64)))
+            self._pages[b].extend(new)
             self._mapped[b] = len(self._pages[b]) * self.page_rows
+        if need > len(self._pages[b]):
+            raise RuntimeError("out of pages")
 
     def _grow_all(self, targets) -> None:
         """Map pages so that sequence b holds n tokens, for (b, n) in targets.
@@ -242,11 +247,16 @@ class INT4PagedSequenceCache:
             self._apply(updates)
 
     def _apply(self, updates: list) -> None:
+        """Write (sequence, first logical page, physical pages) runs into the
+        device page table with one scatter."""
         import torch
         if not updates:
             return
-        u = torch.tensor(updates, dtype=torch.int64).cuda()
-        self.page_table[u[:, 0], u[:, 1]] = u[:, 2].to(torch.int32)
+        seq = np.concatenate([np.full(len(p), b, np.int64) for b, _, p in updates])
+        col = np.concatenate([np.arange(lp, lp + len(p), dtype=np.int64) for _, lp, p in updates])
+        phys = np.concatenate([p for _, _, p in updates])
+        u = torch.from_numpy(np.stack([seq, col, phys])).cuda()
+        self.page_table[u[0], u[1]] = u[2].to(torch.int32)
 
     def _sync_if_stepped(self) -> None:
         # step() advances the lengths on the device only; host-side page
@@ -254,44 +264,84 @@ class INT4PagedSequenceCache:
         if self._unsynced_steps:
             self.sync_lengths()
 
-    def free(self, b: int) -> None:
-        """Release sequence b's pages; its slot starts empty."""
-        self._sync_if_stepped()
+    def _release(self, b: int) -> None:
+        """Host side of free(): sequence b's pages go back to the free list."""
         self._free.extend(reversed(self._pages[b]))
         self._pages[b] = []
         self._mapped[b] = 0
         self._lens[b] = 0
+
+    def free(self, b: int) -> None:
+        """Release sequence b's pages; its slot starts empty."""
+        self._sync_if_stepped()
+        self._release(b)
         self.seq_lens[b] = 0
 
     # ---- writes ------------------------------------------------------------
 
-    def prefill(self, k, v, seq_lens) -> None:
-        """Start sequences 0..B-1 from k, v [B, kv_heads, T, D] (keys float32,
-        values in the cache's dtype) with seq_lens[b] <= T valid tokens."""
+    def _check_prefill(self, k, v, lens) -> None:
+        """Every condition prefill() and the quantizer need, checked before
+        the cache is touched, so a rejected call leaves it as it was."""
         import torch
-        lens = np.asarray(seq_lens.cpu() if hasattr(seq_lens, "cpu") else seq_lens, np.int64)
+        if not isinstance(k, torch.Tensor) or not isinstance(v, torch.Tensor):
+            raise TypeError("k and v must be torch tensors on the GPU")
+        if k.dim() != 4 or tuple(v.shape) != tuple(k.shape):
+            raise ValueError("k and v must be [batch, kv_heads, tokens, head_dim] of this cache")
         B, H, T, D = k.shape
-        if (H, D) != (self.num_kv_heads, self.head_dim) or tuple(v.shape) != tuple(k.shape):
+        if (H, D) != (self.num_kv_heads, self.head_dim):
             raise ValueError("k and v must be [batch, kv_heads, tokens, head_dim] of this cache")
         if B > self.max_seqs or len(lens) != B or (lens < 0).any() or (lens > T).any():
             raise ValueError("bad batch size or sequence lengths")
+        cap = self.max_pages_per_seq * self.page_rows
+        if (lens > cap).any():
+            raise ValueError(f"a sequence of {int(lens.max())} tokens exceeds the "
+                             f"{cap} tokens per sequence this cache holds")
+        if not (k.is_cuda and v.is_cuda):
+            raise RuntimeError("k and v must be GPU (cuda device) tensors")
+        if k.dtype != torch.float32:
+            raise TypeError(f"k must be float32, got {k.dtype}")
+        if (k.stride(3) != 1 or k.data_ptr() % 16
+                or any((k.stride(i) * 4) % 16 for i in range(3))):
+            raise ValueError("k needs contiguous rows starting on 16-byte boundaries")
+        if v.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise TypeError(f"v must be float32, float16 or bfloat16, got {v.dtype}")
+        need = int(((lens + self.page_rows - 1) // self.page_rows).sum())
+        held = sum(len(self._pages[b]) for b in range(B))
+        if need > len(self._free) + held:
+            raise RuntimeError(f"out of pages: the batch needs {need}, "
+                               f"{len(self._free) + held} are free or held by it")
+
+    def prefill(self, k, v, seq_lens) -> None:
+        """Start sequences 0..B-1 from k, v [B, kv_heads, T, D] (keys float32,
+        values converted to the cache's dtype) with seq_lens[b] <= T valid
+        tokens. Raises before changing the cache when an argument is
+        unusable."""
+        import torch
+        lens = np.asarray(seq_lens.cpu() if hasattr(seq_lens, "cpu") else seq_lens, np.int64)
+        lens = lens.reshape(-1)
+        self._check_prefill(k, v, lens)
+        B, _, T, _ = k.shape
         self._sync_if_stepped()
         for b in range(B):
-            self.free(b)
-        self._grow_all((b, int(lens[b])) for b in range(B))
+            self._release(b)
+        try:
+            self._grow_all((b, int(lens[b])) for b in range(B))
+        except Exception:
+            self.seq_lens[:B] = 0  # the released slots are empty on the device too
+            raise
         lens_t = torch.as_tensor(lens, dtype=torch.int32).cuda()
         self.seq_lens[:B] = lens_t
         self._lens[:B] = lens
         ops.quantize_int4_paged(k, self.seq_lens[:B], self.page_table[:B], self.k_pages,
                                 self.k_scale[:B], self.k_zp[:B], self.group_rows)
-        # Values: token t of sequence b -> page_table[b, t // page_rows], row t % page_rows.
-        bi, ti = np.nonzero(np.arange(T)[None, :] < lens[:, None])
-        if len(bi):
-            pages = torch.as_tensor(np.array([self._pages[b][t // self.page_rows]
-                                              for b, t in zip(bi, ti)]), device="cuda")
-            rows = torch.as_tensor(ti % self.page_rows, device="cuda")
-            bt, tt = torch.as_tensor(bi, device="cuda"), torch.as_tensor(ti, device="cuda")
-            self.v_pages[pages, :, rows, :] = v[bt, :, tt, :].to(self.v_pages.dtype)
+        # Values: token t of sequence b -> row t % page_rows of physical page
+        # page_table[b, t // page_rows], gathered and scattered on the device.
+        if T and lens.any():
+            dev = self.seq_lens.device
+            t = torch.arange(T, device=dev)
+            bi, ti = torch.nonzero(t[None, :] < lens_t[:, None], as_tuple=True)
+            pages = self.page_table[bi, ti // self.page_rows].long()
+            self.v_pages[pages, :, ti % self.page_rows, :] = v[bi, :, ti, :].to(self.v_pages.dtype)
         # Open groups: the float keys of each sequence's partial last group.
         for b in range(B):
             r = int(lens[b]) % self.group_rows

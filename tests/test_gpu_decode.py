@@ -399,7 +399,7 @@ class TestGroupedQueryHeads:
     @pytest.mark.parametrize("D,rep,vdtype", [(128, 4, None), (64, 8, None), (128, 2, None),
                                               (128, 8, None), (128, 8, "float16"),
                                               (64, 4, "float16"), (128, 4, "bfloat16")])
-    def test_matrix_core_equals_vector_kernel(self, monkeypatch, D, rep, vdtype):
+    def test_matrix_core_equals_vector_kernel(self, D, rep, vdtype):
         """The int8 matrix-core kernel's logits are exact up to the 41-bit
         rounding of q*s; it agrees with the vector grouped kernel (fp64
         products) to float32 rounding."""
@@ -409,12 +409,13 @@ class TestGroupedQueryHeads:
         q_t, kp, v_t, s, z, pt, sl = _paged_device(
             w, value_dtype=getattr(torch, vdtype) if vdtype else None)
         q = torch.randn(2, 2 * rep, D, device="cuda", generator=torch.Generator("cuda").manual_seed(7))
+        from flash_decode_int4 import capi
         mfma = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=2)
-        monkeypatch.setenv("FDI4_DECODE_MFMA", "0")
-        vec = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=2)
+        with capi.tuning(decode_vector_only=1):
+            vec = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=2)
         assert (mfma - vec).abs().max().item() < 2e-6
 
-    def test_grouped_equals_per_head_kernel(self, monkeypatch):
+    def test_grouped_equals_per_head_kernel(self):
         """The grouped and the per-head kernel compute the same logits up to
         fp64 rounding (other channel partitions per lane); the outputs agree to
         float32 rounding."""
@@ -423,9 +424,10 @@ class TestGroupedQueryHeads:
         w = make_workload(batch=2, heads=4, head_dim=128, seq_lens=[2048, 999], seed=21)
         q_t, kp, v_t, s, z, pt, sl = _paged_device(w)
         q = torch.randn(2, 16, 128, device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+        from flash_decode_int4 import capi
         grouped = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=1)
-        monkeypatch.setenv("FDI4_DECODE_HEADS_PER_WG", "1")
-        per_head = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=1)
+        with capi.tuning(decode_heads_per_wg=1):
+            per_head = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=1)
+            again = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=1)
         assert (grouped - per_head).abs().max().item() < 2e-6
-        again = _ops().flash_decode_paged(q, kp, v_t, s, z, pt, sl, num_splits=1)
         assert torch.equal(per_head, again)

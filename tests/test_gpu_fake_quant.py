@@ -1,23 +1,15 @@
 """Device quantize-dequantize of keys for quality studies (reference
-scripts/validate_llama.py:126-178).
+scripts/validate_llama.py:126-154).
 
 * bit-exact with the oracle for float32, float16 and bfloat16 keys, both
   roundings, both scale forms, partial blocks, head sizes whose 16-byte
   vectors do not divide the workgroup, blocks held in registers and blocks
   read twice, block size 1, strided and misaligned views;
-* each scale form equals the harness's formula as eager torch operations on
+* each scale form equals the study's formula as eager torch operations on
   the GPU (a Python-scalar divisor there is a reciprocal multiply);
 * the C ABI entry point gives the binding's bytes and rejects misaligned rows;
 * at full size (8 x 32 x 2048 x 128 float32 keys): block size 1 is the
-  identity under half-up, and sampled streams match the oracle;
-* through a transformers Llama model with random weights: the quantizing
-  cache fires once per layer, and the logits equal those of a cache that
-  hands attention the oracle's quantized keys;
-* the perplexity driver keeps the reference harness's contract (its tests,
-  tests/test_perplexity_harness.py:44-180, on the GPU): INT4 keys change the
-  loss, one hook call per layer per window, grouped KV heads, the
-  full-precision path untouched, errors when the hook never fires or changes
-  nothing.
+  identity under half-up, and sampled streams match the oracle.
 """
 
 import ctypes
@@ -242,143 +234,3 @@ def test_full_size_identity_and_sampled_streams():
                                       _expected_bits(kk, 256, "half_up"))
     del k, out
     torch.cuda.empty_cache()
-
-
-def test_quantizing_cache_in_a_llama_model():
-    """A 2-layer Llama (random weights, float32, eager attention): the hook fires
-    once per layer and changes the keys; the logits equal those computed
-    with the oracle's quantized keys handed to attention."""
-    import torch
-    transformers = pytest.importorskip("transformers")
-    from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM
-    from flash_decode_int4.quality import make_key_quantizing_cache
-
-    cfg = LlamaConfig(vocab_size=256, hidden_size=128, intermediate_size=256,
-                      num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
-                      max_position_embeddings=1024)
-    cfg._attn_implementation = "eager"
-    torch.manual_seed(0)
-    model = LlamaForCausalLM(cfg).cuda().eval()
-    ids = torch.randint(0, 256, (1, 300), device="cuda")
-
-    stats = {}
-    with torch.no_grad():
-        got = model(ids, past_key_values=make_key_quantizing_cache(128, stats),
-                    use_cache=True).logits
-        plain = model(ids, past_key_values=DynamicCache(), use_cache=True).logits
-    assert stats["hook_calls"] == cfg.num_hidden_layers
-    assert stats["max_abs_key_change"] > 0.0
-
-    oracle_cache = DynamicCache()
-    inner = oracle_cache.update
-
-    def update(key_states, value_states, layer_idx, *args, **kwargs):
-        k, v = inner(key_states, value_states, layer_idx, *args, **kwargs)
-        dq = fake_quantize_keys_ref(k.float().cpu().numpy(), 128, "half_up")
-        return torch.from_numpy(dq).to(k.device, k.dtype), v
-
-    oracle_cache.update = update
-    with torch.no_grad():
-        want = model(ids, past_key_values=oracle_cache, use_cache=True).logits
-    assert torch.equal(got, want)
-    assert not torch.equal(got, plain)
-    assert bool(torch.isfinite(got).all())
-
-
-# ---- the perplexity harness (reference tests/test_perplexity_harness.py) ----
-
-def _tiny_llama(kv_heads=4, layers=2, seed=0):
-    """Random-weight Llama in float32 with eager attention, on the GPU."""
-    import torch
-    from transformers import LlamaConfig, LlamaForCausalLM
-    torch.manual_seed(seed)
-    cfg = LlamaConfig(vocab_size=512, hidden_size=128, intermediate_size=256,
-                      num_hidden_layers=layers, num_attention_heads=4,
-                      num_key_value_heads=kv_heads, max_position_embeddings=2048)
-    cfg._attn_implementation = "eager"
-    return LlamaForCausalLM(cfg).cuda().eval()
-
-
-def _ids(n, seed=1):
-    import torch
-    g = torch.Generator().manual_seed(seed)
-    return torch.randint(0, 512, (1, n), generator=g).cuda()
-
-
-class TestPerplexityHarness:
-
-    def test_int4_keys_change_the_loss(self):
-        from flash_decode_int4.quality import perplexity
-        model, ids = _tiny_llama(), _ids(600)
-        base = perplexity(model, ids, quantize_keys=False)
-        int4 = perplexity(model, ids, quantize_keys=True)
-        assert int4["ppl"] != base["ppl"]
-        assert int4["max_abs_key_change"] > 0
-        assert np.isfinite(int4["ppl"])
-
-    def test_hook_fires_once_per_layer_per_window(self):
-        from flash_decode_int4.quality import perplexity
-        model, ids = _tiny_llama(layers=3), _ids(600)
-        r = perplexity(model, ids, quantize_keys=True, max_length=256, stride=128)
-        assert r["windows"] > 1
-        assert r["hook_calls"] == 3 * r["windows"]
-
-    def test_grouped_query_attention_and_both_roundings(self):
-        from flash_decode_int4.quality import perplexity
-        model, ids = _tiny_llama(kv_heads=2), _ids(400)
-        base = perplexity(model, ids, quantize_keys=False)
-        up = perplexity(model, ids, quantize_keys=True)
-        even = perplexity(model, ids, quantize_keys=True, rounding="half_even")
-        assert up["ppl"] != base["ppl"] and even["ppl"] != base["ppl"]
-        assert np.isfinite(up["ppl"]) and np.isfinite(even["ppl"])
-
-    def test_full_precision_path_is_untouched(self):
-        import torch
-        from flash_decode_int4.quality import perplexity
-        model, ids = _tiny_llama(), _ids(300)
-        with torch.no_grad():
-            direct = float(model(ids, labels=ids).loss)
-        r = perplexity(model, ids, quantize_keys=False, max_length=2048, stride=1024)
-        assert abs(np.log(r["ppl"]) - direct) < 1e-5
-
-    def test_window_with_nothing_to_score_adds_nothing(self):
-        """n = max_length + 1 with stride = max_length: the last window holds one
-        fresh token and no shifted target; the result is the first window's."""
-        from flash_decode_int4.quality import perplexity
-        model, ids = _tiny_llama(), _ids(257)
-        r = perplexity(model, ids, quantize_keys=True, max_length=256, stride=256)
-        first = perplexity(model, ids[:, :256], quantize_keys=True, max_length=256,
-                           stride=256)
-        assert r["windows"] == 2 and np.isfinite(r["ppl"])
-        assert r["tokens"] == first["tokens"] == 255
-        assert r["ppl"] == first["ppl"]
-
-    def test_raises_when_attention_bypasses_the_cache(self):
-        import torch
-        from flash_decode_int4.quality import perplexity
-
-        class BypassesCache(torch.nn.Module):
-            def forward(self, ids, labels=None, use_cache=True, past_key_values=None):
-                class Out:
-                    loss = torch.tensor(1.0)
-                return Out()
-
-        with pytest.raises(RuntimeError, match="never fired"):
-            perplexity(BypassesCache(), _ids(64), quantize_keys=True)
-
-    def test_raises_when_keys_are_left_unchanged(self, monkeypatch):
-        from flash_decode_int4 import quality
-        monkeypatch.setattr(quality, "fake_quantize_keys", lambda k, *a, **kw: k)
-        with pytest.raises(RuntimeError, match="unchanged"):
-            quality.perplexity(_tiny_llama(), _ids(200), quantize_keys=True)
-
-    def test_cache_factory_returns_a_working_cache(self):
-        import torch
-        from flash_decode_int4.quality import make_key_quantizing_cache
-        stats = {"hook_calls": 0, "max_abs_key_change": 0.0}
-        cache = make_key_quantizing_cache(256, stats)
-        k = torch.randn(1, 2, 10, 8, device="cuda")
-        kq, v = cache.update(k, k.clone(), 0)
-        assert stats["hook_calls"] == 1
-        assert kq.shape == k.shape and v.shape == k.shape
-        np.testing.assert_array_equal(_bits(kq), _expected_bits(k, 256, "half_up"))

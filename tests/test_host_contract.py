@@ -276,58 +276,136 @@ class TestCABI:
         assert lib.fdi4_decode_num_splits(8, 32, cache) == 4
 
     def test_invalid_arguments_are_rejected_before_any_device_call(self):
-        from flash_decode_int4 import capi
-        lib = capi.load()
-        bad = 1  # hipErrorInvalidValue
-        assert lib.fdi4_quantize_rows(None, 4, 4, 4, None, 4, 0, None, None, None, 0, None) == bad
-        assert lib.fdi4_decode_paged(None, 1, 1, 0, 0, None, None, 0, 0, 0, None, 0, None) == bad
-        cache = capi.PagedCache(head_dim=96, page_rows=16, num_kv_heads=1, pages_per_group=1,
-                                max_pages=1, num_pages=1, k_pages=16, k_scale=16, k_zp=16)
-        assert lib.fdi4_quantize_paged(16, 1, 16, 0, 0, 128, 128, cache, None) == bad
-        assert lib.fdi4_merge_splits(None, None, 1, 1, 128, 1, None, 0, 0, None) == bad
-        assert lib.fdi4_flash_decode_int4_ws(None, None, None, None, None, None, 1, 1, 300, 1, 1,
-                                             None, None, 0, None) == bad
-        # Row strides whose 16-row chunk does not fit in 31 bits of byte
-        # offset (the kernels address a chunk's rows with 32-bit offsets).
-        big = capi.PagedCache(head_dim=128, page_rows=16, num_kv_heads=1, pages_per_group=8,
-                              max_pages=8, num_pages=8, k_pages=256, k_scale=256, k_zp=256,
-                              k_page_stride=1 << 30, k_row_stride=1 << 27,
-                              v_pages=256, v_dtype=capi.V_F32, v_page_stride=1 << 12,
-                              v_row_stride=128, s_group_stride=128, seq_lens=256)
-        q = ctypes.c_void_p(256)
-        assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
-                                     None, 0, None) == bad
-        big.k_row_stride = 64
-        big.v_row_stride = 1 << 25
-        assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
-                                     None, 0, None) == bad
-        # Sequences of 2^32 token positions (max_pages x page_rows) do not fit
-        # the kernels' 32-bit token indices.
-        big.v_row_stride = 128
-        big.page_rows, big.max_pages, big.pages_per_group = 32, 1 << 27, 4
-        big.page_table, big.pt_batch_stride = 256, 1 << 27
-        assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
-                                     None, 0, None) == bad
-        assert lib.fdi4_append_paged(q, 128, 128, q, 128, 128, 1, q, 1 << 14, 1 << 14, 128,
-                                     128, ctypes.byref(big), None) == bad
+        _run_with_no_gpu("check_invalid_arguments_are_rejected")
 
     def test_typed_decode_rejects_unknown_element_types(self):
-        """fdi4_decode_paged_ex: query and output types are 0, 1, 2 (float32,
-        float16, bfloat16); value pages fp32, fp16 or bf16; anything else is
-        refused before any device call."""
+        _run_with_no_gpu("check_typed_decode_rejects_unknown_element_types")
+
+    def test_tuning_knobs_are_explicit_and_validated(self):
+        """Launch-shape overrides go through fdi4_set_tuning (the library
+        reads no environment); out-of-range values are refused and leave the
+        knob unchanged; the context manager restores the previous values."""
         from flash_decode_int4 import capi
         lib = capi.load()
-        bad = 1
-        ok_cache = capi.PagedCache(head_dim=128, page_rows=16, num_kv_heads=1, pages_per_group=8,
-                                   max_pages=8, num_pages=8, k_pages=256, k_scale=256, k_zp=256,
-                                   k_page_stride=1024, k_row_stride=64, v_pages=256,
-                                   v_dtype=capi.V_BF16, v_page_stride=2048, v_row_stride=128,
-                                   s_group_stride=128, seq_lens=256)
-        q = ctypes.c_void_p(256)
-        for q_dtype, o_dtype in ((3, 0), (0, 3), (-1, 1), (2, 7)):
-            assert lib.fdi4_decode_paged_ex(q, q_dtype, 1, 1, 128, 128, ctypes.byref(ok_cache),
-                                            q, o_dtype, 128, 128, 1, None, 0, None) == bad
-        ok_cache.v_dtype = 3
-        assert lib.fdi4_decode_paged_ex(q, 1, 1, 1, 128, 128, ctypes.byref(ok_cache), q, 1,
-                                        128, 128, 1, None, 0, None) == bad
-        assert capi.V_BF16 == 2 and capi.K_BF16 == 2
+        for knob in capi.TUNE.values():
+            assert lib.fdi4_get_tuning(knob) == 0
+        assert lib.fdi4_get_tuning(99) == -1 and lib.fdi4_set_tuning(99, 1) == 1
+        waves = capi.TUNE["decode_waves"]
+        assert lib.fdi4_set_tuning(waves, 6) == 1 and lib.fdi4_get_tuning(waves) == 0
+        with capi.tuning(decode_waves=4, decode_heads_per_wg=2):
+            assert lib.fdi4_get_tuning(waves) == 4
+            assert lib.fdi4_get_tuning(capi.TUNE["decode_heads_per_wg"]) == 2
+            cache = capi.PagedCache(max_pages=32, page_rows=16, num_kv_heads=32, head_dim=128)
+            # 4 waves x 8 chunks each: B8 H32 now needs two splits for ~2048 waves.
+            assert lib.fdi4_decode_num_splits(8, 32, cache) == 2
+        assert lib.fdi4_get_tuning(waves) == 0
+        with pytest.raises(ValueError):
+            capi.tuning(decode_wave=4)
+        with pytest.raises(RuntimeError):
+            with capi.tuning(decode_vector_only=2):
+                pass
+        text = open(os.path.join(ROOT, "int4-kv-cache-quantization-cuda-triton-pallas_amd",
+                                 "csrc", "capi.hip")).read()
+        assert "getenv" not in text
+
+
+# The rejection checks pass fake device addresses to calls that are otherwise
+# valid. On a host with a GPU they run in a child process that sees none, so a
+# host check that regressed makes the call fail there instead of launching a
+# kernel on those addresses.
+
+_CHILD = """
+import ctypes, sys
+sys.path[:0] = {paths!r}
+hip = ctypes.CDLL("libamdhip64.so")
+n = ctypes.c_int(-1)
+rc = hip.hipGetDeviceCount(ctypes.byref(n))
+if rc == 0 and n.value > 0:
+    print("SKIP: a GPU is still visible with HIP_VISIBLE_DEVICES/ROCR_VISIBLE_DEVICES hidden")
+    sys.exit(0)
+import importlib.util
+spec = importlib.util.spec_from_file_location("host_contract_child", {path!r})
+mod = importlib.util.module_from_spec(spec)
+spec.loader.exec_module(mod)
+mod.{fn}()
+print("PASS")
+"""
+
+
+def _run_with_no_gpu(fn_name):
+    import subprocess
+    import sys
+    import torch
+    if torch.cuda.device_count() == 0:       # counting does not initialize a device
+        globals()[fn_name]()
+        return
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="-1", ROCR_VISIBLE_DEVICES="-1",
+               CUDA_VISIBLE_DEVICES="-1")
+    paths = [ROOT, os.path.join(ROOT, "tests"),
+             os.path.join(ROOT, "int4-kv-cache-quantization-cuda-triton-pallas_amd")]
+    code = _CHILD.format(paths=paths, path=os.path.abspath(__file__), fn=fn_name)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    if "SKIP:" in r.stdout:
+        pytest.skip(r.stdout.strip())
+    assert "PASS" in r.stdout, r.stdout + r.stderr
+
+
+def check_invalid_arguments_are_rejected():
+    from flash_decode_int4 import capi
+    lib = capi.load()
+    bad = 1  # hipErrorInvalidValue
+    assert lib.fdi4_quantize_rows(None, 4, 4, 4, None, 4, 0, None, None, None, 0, None) == bad
+    assert lib.fdi4_decode_paged(None, 1, 1, 0, 0, None, None, 0, 0, 0, None, 0, None) == bad
+    cache = capi.PagedCache(head_dim=96, page_rows=16, num_kv_heads=1, pages_per_group=1,
+                            max_pages=1, num_pages=1, k_pages=16, k_scale=16, k_zp=16)
+    assert lib.fdi4_quantize_paged(16, 1, 16, 0, 0, 128, 128, cache, None) == bad
+    assert lib.fdi4_merge_splits(None, None, 1, 1, 128, 1, None, 0, 0, None) == bad
+    assert lib.fdi4_flash_decode_int4_ws(None, None, None, None, None, None, 1, 1, 300, 1, 1,
+                                         None, None, 0, None) == bad
+    # Row strides whose 16-row chunk does not fit in 31 bits of byte
+    # offset (the kernels address a chunk's rows with 32-bit offsets).
+    big = capi.PagedCache(head_dim=128, page_rows=16, num_kv_heads=1, pages_per_group=8,
+                          max_pages=8, num_pages=8, k_pages=256, k_scale=256, k_zp=256,
+                          k_page_stride=1 << 30, k_row_stride=1 << 27,
+                          v_pages=256, v_dtype=capi.V_F32, v_page_stride=1 << 12,
+                          v_row_stride=128, s_group_stride=128, seq_lens=256)
+    q = ctypes.c_void_p(256)
+    assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
+                                 None, 0, None) == bad
+    big.k_row_stride = 64
+    big.v_row_stride = 1 << 25
+    assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
+                                 None, 0, None) == bad
+    # Sequences of 2^32 token positions (max_pages x page_rows) do not fit
+    # the kernels' 32-bit token indices.
+    big.v_row_stride = 128
+    big.page_rows, big.max_pages, big.pages_per_group = 32, 1 << 27, 4
+    big.page_table, big.pt_batch_stride = 256, 1 << 27
+    assert lib.fdi4_decode_paged(q, 1, 1, 128, 128, ctypes.byref(big), q, 128, 128, 1,
+                                 None, 0, None) == bad
+    assert lib.fdi4_append_paged(q, 128, 128, q, 128, 128, 1, q, 1 << 14, 1 << 14, 128,
+                                 128, ctypes.byref(big), None) == bad
+
+
+def check_typed_decode_rejects_unknown_element_types():
+    """fdi4_decode_paged_ex: query and output types are 0, 1, 2 (float32,
+    float16, bfloat16); value pages fp32, fp16 or bf16; anything else is
+    refused before any device call."""
+    from flash_decode_int4 import capi
+    lib = capi.load()
+    bad = 1
+    ok_cache = capi.PagedCache(head_dim=128, page_rows=16, num_kv_heads=1, pages_per_group=8,
+                               max_pages=8, num_pages=8, k_pages=256, k_scale=256, k_zp=256,
+                               k_page_stride=1024, k_row_stride=64, v_pages=256,
+                               v_dtype=capi.V_BF16, v_page_stride=2048, v_row_stride=128,
+                               s_group_stride=128, seq_lens=256)
+    q = ctypes.c_void_p(256)
+    for q_dtype, o_dtype in ((3, 0), (0, 3), (-1, 1), (2, 7)):
+        assert lib.fdi4_decode_paged_ex(q, q_dtype, 1, 1, 128, 128, ctypes.byref(ok_cache),
+                                        q, o_dtype, 128, 128, 1, None, 0, None) == bad
+    ok_cache.v_dtype = 3
+    assert lib.fdi4_decode_paged_ex(q, 1, 1, 1, 128, 128, ctypes.byref(ok_cache), q, 1,
+                                    128, 128, 1, None, 0, None) == bad
+    assert capi.V_BF16 == 2 and capi.K_BF16 == 2
