@@ -248,6 +248,27 @@ int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
                                const fdi4_paged_cache* cache, int num_splits, void* partials,
                                size_t partials_bytes, hipStream_t stream);
 
+/* Largest split-partials size fdi4_decode_paged_noalloc holds:
+ * fdi4_decode_workspace_bytes(batch, num_q_heads, head_dim, splits) must not
+ * exceed it (at head_dim 128: 528 bytes per (sequence, q-head, split), about
+ * 15,800 of them). */
+#define FDI4_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* fdi4_decode_paged without a workspace argument and without any allocation:
+ * with more than one split the partials go to a static device array of
+ * FDI4_NOALLOC_SCRATCH_BYTES that the library holds on each GPU (its address
+ * is looked up on the first call on a device). A call whose partials would
+ * exceed the array returns hipErrorInvalidValue before any device work. The
+ * caller still passes the inputs and the output. Calls that overlap on one GPU
+ * (concurrent streams, or threads) share the array and race; serialize them.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, allocation-free serving loops). */
+int fdi4_decode_paged_noalloc(const float* query, int batch, int num_q_heads,
+                              int64_t q_batch_stride, int64_t q_head_stride,
+                              const fdi4_paged_cache* cache, float* out,
+                              int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                              hipStream_t stream);
+
 /* Log-sum-exp merge of split partials part_acc [B, Hq, S, D] fp32 and
  * part_ml [B, Hq, S, 2] fp64 (m, l), as written by fdi4_decode_paged, into
  * out. Exposed so that partials gathered from several devices can be merged.

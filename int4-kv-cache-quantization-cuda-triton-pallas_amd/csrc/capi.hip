@@ -563,6 +563,87 @@ int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
   return launch_decode_any(a, cache->head_dim, cache->v_dtype, batch, stream);
 }
 
+}  // extern "C"
+
+// ---- decode with its split partials in a static device array ------------------
+
+namespace {
+
+// Split partials of fdi4_decode_paged_noalloc. Every GPU the library runs on
+// holds its own copy of this array until the process ends. In host code the
+// name stands for a host-side shadow, not a device address: kernels and
+// copies get the per-device address from scratch_address() instead.
+static __device__ __align__(256) unsigned char scratch[FDI4_NOALLOC_SCRATCH_BYTES];
+
+// Device address of `scratch` on device `dev`, looked up once per device
+// (hipGetSymbolAddress with that device current) and kept.
+hipError_t scratch_address(int dev, void** out) {
+  static std::mutex mu;
+  static std::map<int, void*> addrs;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = addrs.find(dev);
+  if (it != addrs.end()) {
+    *out = it->second;
+    return hipSuccess;
+  }
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return e;
+  if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (cur != dev) {
+    const hipError_t r = hipSetDevice(cur);
+    if (e == hipSuccess) e = r;
+  }
+  if (e != hipSuccess) return e;
+  if (!p) return hipErrorInvalidSymbol;
+  addrs[dev] = p;
+  *out = p;
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fdi4_decode_paged_noalloc(const float* query, int batch, int num_q_heads,
+                              int64_t q_batch_stride, int64_t q_head_stride,
+                              const fdi4_paged_cache* cache, float* out,
+                              int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                              hipStream_t stream) {
+  DecodeArgs a;
+  int rc = make_decode_args(query, FDI4_K_F32, batch, num_q_heads, q_batch_stride,
+                            q_head_stride, cache, num_splits, &a);
+  if (rc != hipSuccess) return rc;
+  if (!out) return hipErrorInvalidValue;
+  const int d = cache->head_dim;
+  a.out = out;
+  a.out_dtype = FDI4_K_F32;
+  a.o_b = out_batch_stride;
+  a.o_h = out_head_stride;
+  if (a.num_splits == 1) {
+    a.final_out = 1;
+    return launch_decode_any(a, d, cache->v_dtype, batch, stream);
+  }
+  // Checked before any device call: partials beyond the array are refused.
+  const size_t need = decode_ws_bytes(batch, num_q_heads, d, a.num_splits);
+  if (need > (size_t)FDI4_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
+  int dev = 0;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  void* base = nullptr;
+  if ((e = scratch_address(dev, &base)) != hipSuccess) return e;
+  // Every split writes its (m, l, acc) whether or not it holds rows, so the
+  // array needs no clearing between calls.
+  rc = carve_partials(base, need, batch, num_q_heads, d, &a);
+  if (rc != hipSuccess) return rc;
+  e = launch_decode_any(a, d, cache->v_dtype, batch, stream);
+  if (e != hipSuccess) return e;
+  return fdi4::launch_merge(a.ws_acc, a.ws_ml, batch, num_q_heads, d, a.num_splits, out,
+                            FDI4_K_F32, out_batch_stride, out_head_stride, stream);
+}
+
 // ---- the reference's dense, shared-stream attention call ----------------------
 
 }  // extern "C"

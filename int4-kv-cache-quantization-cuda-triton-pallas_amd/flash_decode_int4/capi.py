@@ -19,6 +19,8 @@ V_BF16 = 2
 K_F32, K_F16, K_BF16 = 0, 1, 2
 ROUND_HALF_UP, ROUND_HALF_EVEN = 0, 1
 SCALE_DIVIDE, SCALE_RECIPROCAL = 0, 1
+#: FDI4_NOALLOC_SCRATCH_BYTES: the split partials fdi4_decode_paged_noalloc holds.
+NOALLOC_SCRATCH_BYTES = 8 << 20
 #: fdi4_tuning_knob codes (launch-shape overrides for measurement and tests).
 TUNE = {"decode_vector_only": 0, "decode_waves": 1, "decode_heads_per_wg": 2,
         "decode_target_waves": 3, "fake_quant_split": 4}
@@ -85,6 +87,9 @@ SIGNATURES = {
     "fdi4_decode_paged_partials": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64,
                                            ctypes.POINTER(PagedCache), c_int, c_void_p,
                                            c_size_t, c_void_p]),
+    "fdi4_decode_paged_noalloc": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64,
+                                          ctypes.POINTER(PagedCache), c_void_p, c_int64,
+                                          c_int64, c_int, c_void_p]),
     "fdi4_merge_splits": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
                                   c_int64, c_int64, c_void_p]),
     "fdi4_pack_int4": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_int64, c_int,

@@ -387,6 +387,17 @@ def check_invalid_arguments_are_rejected():
                                  None, 0, None) == bad
     assert lib.fdi4_append_paged(q, 128, 128, q, 128, 128, 1, q, 1 << 14, 1 << 14, 128,
                                  128, ctypes.byref(big), None) == bad
+    # Split partials larger than the no-allocation decode's static array
+    # (B64 x Hq64 x 2 splits at D=256: 8 MiB + 128 KiB) are refused.
+    wide = capi.PagedCache(head_dim=256, page_rows=16, num_kv_heads=64, pages_per_group=8,
+                           max_pages=8, num_pages=8, k_pages=256, k_scale=256, k_zp=256,
+                           k_page_stride=1 << 16, k_head_stride=1 << 10, k_row_stride=128,
+                           v_pages=256, v_dtype=capi.V_F32, v_page_stride=1 << 20,
+                           v_head_stride=1 << 12, v_row_stride=256, s_batch_stride=1 << 17,
+                           s_head_stride=1 << 11, s_group_stride=256, seq_lens=256)
+    assert lib.fdi4_decode_workspace_bytes(64, 64, 256, 2) > capi.NOALLOC_SCRATCH_BYTES
+    assert lib.fdi4_decode_paged_noalloc(q, 64, 64, 1 << 14, 256, ctypes.byref(wide), q,
+                                         1 << 14, 256, 2, None) == bad
 
 
 def check_typed_decode_rejects_unknown_element_types():
