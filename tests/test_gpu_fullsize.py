@@ -1,26 +1,39 @@
-"""The path at the benchmark's full sizes (B8 H32 D128 T2048; the
-context-length sweep B8 H32 D128 at T = 512, 8192 and 32768, the last a
-4.3 GB value pool; B64 H32 D128 T4096, also a 4.3 GB pool whose byte offsets
-pass 2^32; ragged B32 up to 8192 tokens), through properties that do not
-depend on size plus sampled streams against the oracle (float32 value pages;
-the anchor also with float16 and bfloat16 value pages; grouped query heads at
-B8 Hkv8 Hq32 T8192):
+"""The path at the benchmark's full sizes, every output checked: the CPU case
+B1 H4 D64 T512; the anchor B8 H32 D128 T2048; the context-length sweep B8 H32
+D128 at T = 512, 8192 and 32768 (the last a 4.3 GB value pool); ragged B32 up
+to 8192 tokens with empty sequences; Llama-2-7B-like B64 H32 D128 T4096 with
+RoPE keys and x20 outlier channels (a 4.3 GB pool whose byte offsets pass
+2^32); the anchor with float16 and bfloat16 value pages; grouped query heads
+at B8 Hkv8 Hq32 T8192.
 
-* the grouped quantizer is bit-exact on sampled (sequence, head) streams;
-* decoding is invariant, bit for bit, under a different physical page
-  permutation of the same logical data (page-table and offset arithmetic);
-* split counts agree (split-K merge);
-* sampled streams of the full decode match the page-loop oracle.
+For every (sequence, head) stream of each workload:
+
+* the grouped quantizer's scales, zero-points and packed pages equal the
+  oracle's, bit for bit;
+* the decode is within 1e-5 (max abs) of the float32 page-loop oracle. A
+  stream whose oracle is itself more than 8e-6 from the float64 arbiter is
+  counted as oracle-limited; for those streams only, the bound is
+  max(1e-5, 1.25 |oracle - float64|). Every stream is also within 1e-5 of
+  the float64 arbiter. Each workload prints one "[parity]" line with the
+  counts and the maxima.
+
+Size-independent properties on top: the decode is invariant, bit for bit,
+under a different physical page permutation of the same logical data, and
+split counts agree.
 """
+
+import json
 
 import numpy as np
 import pytest
 
-from oracle import pack_int4, paged_decode_f64, paged_decode_ref, quantize_groups_ref
+from oracle.pool import paged_oracle_all
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-5
+TOL = 1e-5            # max abs error against the float32 oracle
+ORACLE_LIMIT = 8e-6   # oracle streams further than this from float64 are oracle-limited
+RELAX = 1.25          # bound on oracle-limited streams: max(TOL, RELAX * |o32 - o64|)
 
 
 def _ops():
@@ -44,35 +57,53 @@ def _build(name, value_dtype="float32"):
     return st
 
 
-def _streams(st, n, seed):
-    """n (sequence, head) pairs with at least one token, chosen at random."""
-    lens = np.asarray(st["w"]["seq_lens"])
-    rng = np.random.RandomState(seed)
-    live = np.nonzero(lens > 0)[0]
-    return [(int(rng.choice(live)), int(rng.randint(st["w"]["heads"]))) for _ in range(n)]
+def _decode(st, **kw):
+    return _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
+                                     st["sl"], **kw)
 
 
-def _stream_problem(st, b, h):
-    """The stream's pages gathered into a one-sequence, one-head paged problem."""
-    n = int(st["w"]["seq_lens"][b])
-    npg = (n + 15) // 16
-    phys = st["w"]["page_table"][b, :npg]
-    kp = st["kp"][phys, h:h + 1].cpu().numpy()
-    vp = st["v"][phys, h:h + 1].float().cpu().numpy()
-    s = st["s"][b:b + 1, h:h + 1].cpu().numpy()
-    z = st["z"][b:b + 1, h:h + 1].cpu().numpy()
-    q = st["q"][b:b + 1, h:h + 1].cpu().numpy()
-    table = np.arange(npg, dtype=np.int32)[None]
-    return (q, kp, vp, s, z, table, np.array([n], np.int32), 16, 128)
-
-
-def torch_index(mask):
+def _check_every_stream(label, st):
+    """Decode on the GPU, the oracle over every stream on the host cores, and
+    the gates of the module docstring; returns the printed record."""
     import torch
-    return torch.as_tensor(np.nonzero(mask)[0], device="cuda")
+    out = _decode(st)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    w = st["w"]
+    host = dict(q=st["q"].cpu().numpy(), kp=st["kp"].cpu().numpy(),
+                v=st["v"].float().cpu().numpy(), s=st["s"].cpu().numpy(),
+                z=st["z"].cpu().numpy(), pt=np.asarray(w["page_table"]),
+                sl=np.asarray(w["seq_lens"]), k=st["k"].cpu().numpy())
+    res = paged_oracle_all(host)
+    del host
+    o32, o64 = res["o32"], res["o64"]
+    lens = np.asarray(w["seq_lens"])
+    live = np.broadcast_to((lens > 0)[:, None], got.shape[:2])
+    e32 = np.abs(got - o32).max(axis=-1)
+    e64 = np.abs(got - o64).max(axis=-1)
+    eo = np.abs(o32 - o64).max(axis=-1)
+    limited = eo > ORACLE_LIMIT
+    strict = ~limited
+    rec = dict(workload=label, streams=int(got.shape[0] * got.shape[1]),
+               live_streams=int(live.sum()), oracle_limited=int(limited.sum()),
+               key_mismatch_streams=res["key_mismatch"],
+               max_hip_vs_o32=float(e32.max()),
+               max_hip_vs_o32_strict_streams=float(e32[strict].max()) if strict.any() else 0.0,
+               max_hip_vs_f64=float(e64.max()), max_o32_vs_f64=float(eo.max()),
+               oracle_workers=res["workers"], oracle_seconds=round(res["seconds"], 2))
+    print("\n[parity] " + json.dumps(rec), flush=True)
+    assert np.isfinite(got).all(), label
+    assert (got[~live] == 0).all(), label                      # empty sequences: exact zeros
+    assert res["key_mismatch"] == 0, rec
+    assert e32[strict].max(initial=0.0) <= TOL, rec
+    assert (e32[limited] <= np.maximum(TOL, RELAX * eo[limited])).all(), rec
+    assert e64.max() <= TOL, rec
+    return rec
 
 
 @pytest.fixture(scope="module",
-                params=["anchor", "sweep_512", "sweep_8192", "sweep_32768", "llama", "ragged"])
+                params=["cpu", "anchor", "sweep_512", "sweep_8192", "sweep_32768", "ragged",
+                        "llama"])
 def built(request):
     import torch
     st = _build(request.param)
@@ -81,38 +112,9 @@ def built(request):
     torch.cuda.empty_cache()
 
 
-def test_quantizer_bit_exact_on_sampled_streams(built):
+def test_every_stream_against_the_oracle(built):
     name, st = built
-    for b, h in _streams(st, 6, seed=1):
-        n = int(st["w"]["seq_lens"][b])
-        k = st["k"][b:b + 1, h:h + 1, :n].cpu().numpy()
-        qr, sr, zr = quantize_groups_ref(k, np.array([n]))
-        ng = (n + 127) // 128
-        np.testing.assert_array_equal(st["s"][b, h, :ng].cpu().numpy(), sr[0, 0, :ng])
-        np.testing.assert_array_equal(st["z"][b, h, :ng].cpu().numpy(), zr[0, 0, :ng])
-        npg = (n + 15) // 16
-        phys = st["w"]["page_table"][b, :npg]
-        got = st["kp"][phys, h].cpu().numpy()                     # [npg, 16, D/2]
-        want = pack_int4(qr[0, 0])                                 # [n, D/2]
-        for lp in range(npg):
-            r = min(16, n - lp * 16)
-            np.testing.assert_array_equal(got[lp, :r], want[lp * 16:lp * 16 + r])
-
-
-def test_decode_matches_oracle_on_sampled_streams(built):
-    name, st = built
-    out = _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
-                                    st["sl"])
-    assert bool(out.isfinite().all())
-    lens = np.asarray(st["w"]["seq_lens"])
-    if (lens == 0).any():
-        assert bool((out[torch_index(lens == 0)] == 0).all())
-    for b, h in _streams(st, 6, seed=2):
-        args = _stream_problem(st, b, h)
-        o32, o64 = paged_decode_ref(*args)[0, 0], paged_decode_f64(*args)[0, 0]
-        got = out[b, h].cpu().numpy()
-        e32, eo = np.abs(got - o32).max(), np.abs(o32 - o64).max()
-        assert e32 <= max(TOL, 1.25 * eo), (name, b, h, e32, eo)
+    _check_every_stream(name, st)
 
 
 def test_page_permutation_invariance(built):
@@ -136,7 +138,7 @@ def test_page_permutation_invariance(built):
     # sequence's length are never written, in either pool).
     assert torch.equal(kp2[perm[used]], st["kp"][used])
     assert torch.equal(s2, st["s"]) and torch.equal(z2, st["z"])
-    a = _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"], st["sl"])
+    a = _decode(st)
     b = _ops().flash_decode_paged(st["q"], kp2, v2, s2, z2, pt2, st["sl"])
     assert torch.equal(a, b)
     del v2, kp2
@@ -147,55 +149,32 @@ def test_split_counts_agree(built):
     up to 8192 rows accumulated in float32 in another order and merged with
     other weights, so a few ulps of the output's magnitude (~1) apart."""
     name, st = built
-    base = _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
-                                     st["sl"], num_splits=1)
+    base = _decode(st, num_splits=1)
     for splits in (4, 16):
-        got = _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
-                                        st["sl"], num_splits=splits)
+        got = _decode(st, num_splits=splits)
         assert (got - base).abs().max().item() < 5e-6, (name, splits)
 
 
 @pytest.mark.parametrize("value_dtype", ["float16", "bfloat16"])
 def test_16bit_values_at_the_anchor(value_dtype):
-    """B8 H32 D128 T2048 with 16-bit value pages: sampled streams of the full
-    decode against the oracle fed the same (widened) values."""
+    """B8 H32 D128 T2048 with 16-bit value pages: every stream against the
+    oracle fed the same (widened) values."""
     import torch
     st = _build("anchor", value_dtype)
     assert st["v"].dtype == getattr(torch, value_dtype)
-    out = _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
-                                    st["sl"])
-    assert out.dtype == torch.float32 and bool(out.isfinite().all())
-    for b, h in _streams(st, 6, seed=3):
-        args = _stream_problem(st, b, h)
-        o32, o64 = paged_decode_ref(*args)[0, 0], paged_decode_f64(*args)[0, 0]
-        got = out[b, h].cpu().numpy()
-        e32, eo = np.abs(got - o32).max(), np.abs(o32 - o64).max()
-        assert e32 <= max(TOL, 1.25 * eo), (value_dtype, b, h, e32, eo)
+    _check_every_stream(f"anchor_{value_dtype}_values", st)
     del st
     torch.cuda.empty_cache()
 
 
 def test_grouped_query_heads_at_full_size():
     """B8 Hkv8 Hq32 D128 T8192 (four q-heads per kv-head: the int8 matrix-core
-    kernel with splits and the merge): sampled (sequence, q-head) streams
-    against the oracle over the kv-head the q-head reads."""
+    kernel with splits and the merge): every (sequence, q-head) stream against
+    the oracle over the kv-head the q-head reads."""
     import torch
     st = _build("gqa")
     w = st["w"]
-    hq, hkv = w["q_heads"], w["heads"]
-    assert st["q"].shape[1] == hq and hq == 4 * hkv
-    out = _ops().flash_decode_paged(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
-                                    st["sl"])
-    assert bool(out.isfinite().all())
-    rng = np.random.RandomState(4)
-    for _ in range(8):
-        b, qh = int(rng.randint(w["batch"])), int(rng.randint(hq))
-        q_, kp, vp, s_, z_, table, n, pr, grp = _stream_problem(st, b, qh // (hq // hkv))
-        q_ = st["q"][b:b + 1, qh:qh + 1].cpu().numpy()
-        args = (q_, kp, vp, s_, z_, table, n, pr, grp)
-        o32, o64 = paged_decode_ref(*args)[0, 0], paged_decode_f64(*args)[0, 0]
-        got = out[b, qh].cpu().numpy()
-        e32, eo = np.abs(got - o32).max(), np.abs(o32 - o64).max()
-        assert e32 <= max(TOL, 1.25 * eo), (b, qh, e32, eo)
+    assert st["q"].shape[1] == w["q_heads"] == 4 * w["heads"]
+    _check_every_stream("gqa", st)
     del st
     torch.cuda.empty_cache()
