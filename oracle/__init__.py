@@ -18,6 +18,9 @@ attention  page-loop online softmax (reference src/flash_decode_ref.py:30-223),
 fakequant  quantize-dequantize of key tensors in blocks (reference
            scripts/validate_llama.py:126-154; half-even form per block of
            src/quantize_int4_ref.py:139-158) and the bfloat16 rounding
+pool       the paged oracle and the key re-quantization over every stream of a
+           workload, spread over the host cores (results identical to the
+           one-process functions)
 cref       ctypes loader for the C restatement in ``oracle/c`` (quantizer,
            packing and a float64 attention arbiter), built by ``oracle/Makefile``
 
