@@ -52,8 +52,15 @@ calibrated by the same counter on a kernel that moves 256 MiB in that
 direction only (a sum for reads, a fill for writes); --no-pmc skips them (and
 must be given when this script itself runs under rocprofv3).
 
+checks.seq_len_plus_1 re-runs the decode with every length + 1 (pages and
+groups one row into fresh ones); its "interleaved" record times the workload
+and the + 1 lengths in alternating blocks, so the two figures share clocks
+and memory state.
+
 Prints ONE JSON line. Options: --workload (anchor, sweep_512 ... llama,
-ragged), --splits, --value-dtype float16|bfloat16, --no-cpu, --no-pmc.
+ragged), --splits, --value-dtype float16|bfloat16, --no-cpu, --no-pmc,
+--decode-only (the decode timing alone: the command whose rocprofv3 kernel
+trace is the profile of the headline loop).
 """
 
 import argparse
@@ -94,6 +101,10 @@ def parse():
     p.add_argument("--cpu-runs", type=int, default=3)
     p.add_argument("--no-pmc", action="store_true",
                    help="skip the rocprofv3 --pmc traffic runs (required under rocprofv3)")
+    p.add_argument("--decode-only", action="store_true",
+                   help="time the decode of the workload and nothing else (no other paths, "
+                        "PMC or CPU legs): the command a rocprofv3 kernel trace of the "
+                        "headline loop runs")
     p.add_argument("--pmc-child", default="", help=argparse.SUPPRESS)
     return p.parse_args()
 
@@ -277,7 +288,10 @@ def hbm_probes():
     return res
 
 
-def time_decode(sets, splits, steps, warmup):
+def decode_launchers(sets, splits):
+    """(S, step, decode_only): the production decode of input set i % len(sets)
+    (decode kernel, plus the merge with S > 1 splits) and the decode kernel
+    alone."""
     import torch
     from flash_decode_int4._lib import load_binding
     C = load_binding()
@@ -307,6 +321,33 @@ def time_decode(sets, splits, steps, warmup):
         st = sets[i % len(sets)]
         C.decode_paged_partials(st["q"], st["kp"], st["v"], st["s"], st["z"], st["pt"],
                                 st["sl"], None, ppg, maxp, S, parts)
+
+    return S, step, decode_only
+
+
+def interleaved_us(fa, fb, rounds=10, block=20):
+    """Per-launch time of two launch sequences measured in alternating blocks
+    (A, B, A, B, ...; one event pair per block of `block` back-to-back
+    launches, a synchronize before each block), so both see the same clocks
+    and memory state; returns the two medians over the rounds."""
+    import torch
+    ta, tb = [], []
+    for r in range(rounds):
+        for fn, out in ((fa, ta), (fb, tb)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for i in range(block):
+                fn(r * block + i)
+            e1.record()
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1) * 1e3 / block)
+    return median(ta), median(tb)
+
+
+def time_decode(sets, splits, steps, warmup):
+    import torch
+    S, step, decode_only = decode_launchers(sets, splits)
 
     def timed(fn, n):
         """n back-to-back launches; one event pair on the launch stream (per-launch
@@ -841,28 +882,8 @@ def main():
         sys.exit(1)
 
     res = time_decode(sets, args.splits, args.steps, args.warmup)
-    qt, qt_median = time_quantizer(sets, args.steps, args.warmup)
-    app = time_append(w0, args.value_dtype, args.steps, args.warmup)
-    probe = hbm_probes()
-    refcfg = time_reference_config(args.steps, args.warmup)
-    refq, refq_host = time_reference_quantizer(args.steps, args.warmup)
-    fq = time_fake_quant(args.steps, args.warmup)
-    other = time_other_paths(args)
-    other["decode_step"] = time_decode_step(args)
-    other["decode_step_small"] = time_decode_step(args, B=1, H=8, D=128, T=1024)
-
-    # No shape specialization (the reference bench re-runs at seq_len + 1): every
-    # length + 1, so pages end one row into a fresh page and groups one row into
-    # a fresh group; the output must be finite and the rate must hold.
-    odd_lens = w0["seq_lens"] + 1
-    odd_sets, odd_bytes = build_sets(args.workload, args.value_dtype, seq_lens=odd_lens)
-    odd = time_decode(odd_sets, args.splits, max(args.steps // 2, 5), args.warmup)
-    odd_ok = bool(torch.isfinite(odd["last_out"]).all())
-    del odd_sets
     dec_us, mrg_us, step_us = res["decode_us"], res["merge_us"], res["step_us"]
     ms_per_step = res["wall_s"] / args.steps * 1e3
-    q_us = qt
-
     line = {
         "metric": METRIC,
         "value": round(set_bytes / (ms_per_step * 1e-3) / 1e9, 2),
@@ -896,6 +917,47 @@ def main():
         "decode_kernel_us": round(dec_us, 3),
         "merge_us": round(mrg_us, 3),
         "hbm_frac": round(set_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(set_bytes / (dec_us * 1e-6) / 1e9, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(set_bytes / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "kernel": decode_kernel_label(w0, args.value_dtype),
+    }
+    if args.decode_only:
+        line["roofline"] = roofline
+        print(json.dumps(line), flush=True)
+        return
+
+    qt, qt_median = time_quantizer(sets, args.steps, args.warmup)
+    app = time_append(w0, args.value_dtype, args.steps, args.warmup)
+    probe = hbm_probes()
+    refcfg = time_reference_config(args.steps, args.warmup)
+    refq, refq_host = time_reference_quantizer(args.steps, args.warmup)
+    fq = time_fake_quant(args.steps, args.warmup)
+    other = time_other_paths(args)
+    other["decode_step"] = time_decode_step(args)
+    other["decode_step_small"] = time_decode_step(args, B=1, H=8, D=128, T=1024)
+
+    # No shape specialization (the reference bench re-runs at seq_len + 1): every
+    # length + 1, so pages end one row into a fresh page and groups one row into
+    # a fresh group; the output must be finite and the rate must hold.
+    odd_lens = w0["seq_lens"] + 1
+    odd_sets, odd_bytes = build_sets(args.workload, args.value_dtype, seq_lens=odd_lens)
+    odd = time_decode(odd_sets, args.splits, max(args.steps // 2, 5), args.warmup)
+    odd_ok = bool(torch.isfinite(odd["last_out"]).all())
+    # The two lengths timed in alternating blocks (the same clocks and memory
+    # state for both; separate loops minutes apart differ by a few percent).
+    _, step_a, _ = decode_launchers(sets, args.splits)
+    _, step_b, _ = decode_launchers(odd_sets, args.splits)
+    base_us, odd_us = interleaved_us(step_a, step_b)
+    del odd_sets, step_b
+    q_us = qt
+
+    line.update({
         "quantizer_us": round(q_us, 3),
         "quantizer_us_median": round(qt_median, 3),
         "quantizer_gbs": round(qbytes / (q_us * 1e-6) / 1e9, 2),
@@ -911,18 +973,13 @@ def main():
             "seq_len_plus_1": {
                 "pass": odd_ok, "max_tokens": int(odd_lens.max()),
                 "decode_us": round(odd["step_us"], 3),
-                "hbm_frac": round(odd_bytes / (odd["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+                "hbm_frac": round(odd_bytes / (odd["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "interleaved": {"anchor_us": round(base_us, 3), "plus_1_us": round(odd_us, 3),
+                                "ratio": round(odd_us / base_us, 4), "rounds": 10,
+                                "launches_per_block": 20}},
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(set_bytes / (dec_us * 1e-6) / 1e9, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(set_bytes / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": decode_kernel_label(w0, args.value_dtype),
-        },
-    }
+        "roofline": roofline,
+    })
     if not args.no_pmc:
         traffic, err = pmc_traffic(args)
         if traffic is not None:

@@ -8,8 +8,9 @@
 // Work decomposition (split-K flash decoding):
 //   grid (num_splits, Hq, B); a workgroup of WAVES wave64s owns one split,
 //   a contiguous range of 16-row chunks of one (sequence, q-head); every wave
-//   takes a contiguous sub-range, keeps its own (m, l, acc) and the waves are
-//   merged through LDS. With one split the workgroup writes the output,
+//   takes an equal contiguous sub-range (the first waves also one chunk each
+//   of the remainder, see wave_chunks), keeps its own (m, l, acc) and the
+//   waves are merged through LDS. With one split the workgroup writes the output,
 //   otherwise (m, l, acc[D]) goes to the workspace and merge_kernel combines
 //   the splits with a log-sum-exp weighting.
 //
@@ -81,8 +82,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   const int n_chunks = pages_of(a, T) * cpp;
   const int c_begin = split * a.chunks_per_split;
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
-  int wc0, wc1;
-  wave_chunks(c_begin, c_end, w, WAVES, wc0, wc1);
+  const WaveRange wr = wave_chunks(c_begin, c_end, w, WAVES);
+  const int wc0 = wr.c0, wc1 = wr.c1;
 
   double m_run = -INFINITY;
   float l_lane = 0.f;
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   int c = wc0;
   ChunkMeta cm, nm;
   U32x4 sz[G::SZL];
-  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, min(ci, wc1 - 1)); };
+  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, wr.chunk_at(min(ci, wc1 - 1))); };
   auto step = [&](const KVec<G::KW>* ck, const U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
     if (cm.group != cur_group) {
       float* szw = sz_s[w];

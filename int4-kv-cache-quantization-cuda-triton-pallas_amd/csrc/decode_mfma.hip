@@ -94,8 +94,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
   const int n_chunks = pages_of(a, T) * cpp;
   const int c_begin = split * a.chunks_per_split;
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
-  int wc0, wc1;
-  wave_chunks(c_begin, c_end, w, WAVES, wc0, wc1);
+  const WaveRange wr = wave_chunks(c_begin, c_end, w, WAVES);
+  const int wc0 = wr.c0, wc1 = wr.c1;
 
   // Softmax state of head n16 (meaningful on head lanes).
   double m_run = -INFINITY;
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
   int c = wc0;
   ChunkMeta cm, nm;
   U32x4 sz[G::SZL];
-  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, min(ci, wc1 - 1)); };
+  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, wr.chunk_at(min(ci, wc1 - 1))); };
   auto step = [&](const KVec<G::KW>* ck, const U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
     if (cm.group != cur_group) {
       float* szw = sz_s[w];
