@@ -31,8 +31,9 @@ bins, scales and zero-points bit for bit against the oracle.
 
 other_paths times the decode with fp16 value pages at the anchor shape and with
 grouped-query heads (B8, 8 kv-heads, 32 q-heads, 8192 tokens), and the serving
-loop's step (append + length advance + decode) on the sequence cache, issued
-eagerly and as a replayed HIP graph.
+loop's step (append + decode + length advance, one launch at these shapes) on
+the sequence cache, issued eagerly and replayed from HIP graphs of one and of
+eight steps, interleaved so that the three forms see the same lengths.
 
 fake_quant times the quality-study kernel (INT4 quantize-dequantize of a key
 tensor in blocks) on a Llama-2-7B-sized perplexity window and on the decode
@@ -551,15 +552,20 @@ def time_other_paths(args):
     return out
 
 
-def time_decode_step(args, B=8, H=32, D=128, T=2048):
+def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8):
     """The serving loop's step on the sequence cache (fp32 values, B sequences
     of H heads from T tokens): append one token per (sequence, kv-head),
-    advance the lengths, decode -- issued eagerly from Python, and as one
-    captured HIP graph replayed (the same kernels without the host's per-call
-    work). Each step adds a token, so the cache grows by one row per step."""
+    decode over the advanced lengths, advance them -- one launch when each
+    (sequence, kv-head) is one decode workgroup (fdi4_decode_step). Timed in
+    rounds, each of `graph_steps` steps issued eagerly from Python, then the
+    same number replayed from a graph holding one step, then one replay of a
+    graph holding `graph_steps` steps (the graph launch's own cost spread over
+    them); every step adds a token, and the interleaving gives the three
+    forms the same lengths. Medians over the rounds, per step."""
     import torch
     from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
-    n = args.warmup + 2 * args.steps + 2
+    rounds = max(4, args.steps // (3 * graph_steps))
+    n = args.warmup + 3 * rounds * graph_steps + 4 * graph_steps
     cache = INT4PagedSequenceCache(num_pages=B * ((T + n) // 16 + 2), num_kv_heads=H, head_dim=D,
                                    max_seqs=B, max_seq_len=T + n)
     g = torch.Generator(device="cuda")
@@ -572,31 +578,39 @@ def time_decode_step(args, B=8, H=32, D=128, T=2048):
     vn = torch.randn(B, H, D, device="cuda", generator=g)
     q = torch.randn(B, H, D, device="cuda", generator=g)
 
-    def timed(fn, steps):
+    def timed(fn, reps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record()
-        for _ in range(steps):
+        for _ in range(reps):
             fn()
         e1.record()
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / steps
+        return e0.elapsed_time(e1) * 1e3
 
     for _ in range(args.warmup):
         cache.step(kn, vn, q)
-    eager = timed(lambda: cache.step(kn, vn, q), args.steps)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        out = cache.step(kn, vn, q)
-    replay = timed(graph.replay, args.steps)
-    ok = bool(torch.isfinite(out).all())
+    graph_1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph_1):
+        out_1 = cache.step(kn, vn, q)
+    graph_k = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph_k):
+        for _ in range(graph_steps):
+            out_k = cache.step(kn, vn, q)
+    eager, rep_1, rep_k = [], [], []
+    for _ in range(rounds):
+        eager.append(timed(lambda: cache.step(kn, vn, q), graph_steps) / graph_steps)
+        rep_1.append(timed(graph_1.replay, graph_steps) / graph_steps)
+        rep_k.append(timed(graph_k.replay, 1) / graph_steps)
+    ok = bool(torch.isfinite(out_1).all()) and bool(torch.isfinite(out_k).all())
     cache.sync_lengths()
-    res = {"workload": f"B{B} H{H} D{D} from {T} tokens, fp32 values: append + length "
-                       "advance + decode per step",
-           "eager_us": round(eager, 3), "graph_replay_us": round(replay, 3), "finite": ok,
-           "final_length": int(cache.lengths()[0])}
-    del cache, graph
+    res = {"workload": f"B{B} H{H} D{D} from {T} tokens, fp32 values: append + decode + "
+                       "length advance per step",
+           "eager_us": round(median(eager), 3), "graph_replay_us": round(median(rep_1), 3),
+           f"graph_{graph_steps}_steps_replay_us_per_step": round(median(rep_k), 3),
+           "rounds": rounds, "finite": ok, "final_length": int(cache.lengths()[0])}
+    del cache, graph_1, graph_k
     torch.cuda.empty_cache()
     return res
 

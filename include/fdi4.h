@@ -174,6 +174,24 @@ int fdi4_append_paged(const float* k_new, int64_t kn_batch_stride, int64_t kn_he
                       int64_t st_row_stride, int group_rows, const fdi4_paged_cache* cache,
                       hipStream_t stream);
 
+/* fdi4_append_paged that also writes lens_next[b] = cache->seq_lens[b] + 1
+ * for every sequence b < batch whose token it appended (seq_lens[b] when the
+ * position falls outside the cache), from one workgroup per sequence; the
+ * cache's own lengths are not changed. lens_next is int32 [batch], 4-byte
+ * aligned, and must not overlap cache->seq_lens[0, batch) (hipErrorInvalidValue
+ * otherwise; cache->seq_lens must be given). With fdi4_decode_paged_advance
+ * reading lens_next and writing the lengths back, one decode step of a
+ * serving loop is two launches with no separate length update, the same
+ * launches every step (so a captured HIP graph replays them unchanged). No
+ * counterpart in the reference, whose cache appends on the host. */
+int fdi4_append_paged_advance(const float* k_new, int64_t kn_batch_stride,
+                              int64_t kn_head_stride, const void* v_new,
+                              int64_t vn_batch_stride, int64_t vn_head_stride, int batch,
+                              float* k_stage, int64_t st_batch_stride, int64_t st_head_stride,
+                              int64_t st_row_stride, int group_rows,
+                              const fdi4_paged_cache* cache, int32_t* lens_next,
+                              hipStream_t stream);
+
 /* Fused INT4 flash decoding with the reference's exact arguments: query
  * [B, H, D], k_q [nb, bs, D] one INT4 value per byte, k_scale/k_zp [nb, D],
  * value [nb, bs, D] fp32, block_lens [nb]; every (b, h) query attends the same
@@ -231,6 +249,47 @@ int fdi4_decode_paged_ex(const void* query, int query_dtype, int batch, int num_
                          const fdi4_paged_cache* cache, void* out, int out_dtype,
                          int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* fdi4_decode_paged_ex that also copies the lengths it reads
+ * (cache->seq_lens[b], b < batch) to lens_out[b] when the decode kernel ends
+ * (int32 [batch], 4-byte aligned, not overlapping cache->seq_lens[0, batch);
+ * cache->seq_lens must be given). The second launch of a serving step:
+ * after fdi4_append_paged_advance(seq_lens = L, lens_next = N), this call
+ * with seq_lens = N and lens_out = L attends over the advanced lengths and
+ * leaves L == N. No counterpart in the reference. */
+int fdi4_decode_paged_advance(const void* query, int query_dtype, int batch, int num_q_heads,
+                              int64_t q_batch_stride, int64_t q_head_stride,
+                              const fdi4_paged_cache* cache, void* out, int out_dtype,
+                              int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                              void* workspace, size_t workspace_bytes, int32_t* lens_out,
+                              hipStream_t stream);
+
+/* One decode step of a serving loop: append token t = cache->seq_lens[b]
+ * of every sequence b < batch (k_new float32 and v_new in the cache's value
+ * type, [batch, num_kv_heads, head_dim] with element strides; the staging
+ * rows k_stage as in fdi4_append_paged), attend with query over the t + 1
+ * rows, and advance cache->seq_lens[b] to t + 1 (t when the sequence is
+ * already at the cache's capacity). The result equals fdi4_append_paged,
+ * a length increment and fdi4_decode_paged_ex, bit for bit.
+ * When each (sequence, kv-head) is one decode workgroup (num_q_heads ==
+ * num_kv_heads and a single split) this is ONE launch: every workgroup
+ * appends its own token and re-quantizes the open group before it decodes,
+ * and the last workgroup of a sequence to finish advances its length
+ * (counters: int32 [batch], zero before the first call, left zero by every
+ * call). Otherwise it is fdi4_append_paged_advance into lens_next (int32
+ * [batch] scratch) and fdi4_decode_paged_advance back, with the library's
+ * split count (workspace of fdi4_decode_workspace_bytes). counters,
+ * lens_next and cache->seq_lens must not overlap. No counterpart in the
+ * reference, whose cache appends on the host. */
+int fdi4_decode_step(const void* query, int query_dtype, int batch, int num_q_heads,
+                     int64_t q_batch_stride, int64_t q_head_stride, const float* k_new,
+                     int64_t kn_batch_stride, int64_t kn_head_stride, const void* v_new,
+                     int64_t vn_batch_stride, int64_t vn_head_stride, float* k_stage,
+                     int64_t st_batch_stride, int64_t st_head_stride, int64_t st_row_stride,
+                     int group_rows, const fdi4_paged_cache* cache, void* out, int out_dtype,
+                     int64_t out_batch_stride, int64_t out_head_stride, int32_t* counters,
+                     int32_t* lens_next, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream);
 
 /* Bytes of the split partials for fdi4_decode_paged_partials: part_acc
  * float [B, Hq, S, D] at offset 0, then part_ml double [B, Hq, S, 2] = (m, l)

@@ -298,11 +298,13 @@ void quantize_paged(torch::Tensor k, torch::Tensor seq_lens, torch::Tensor page_
 }
 
 // One token per sequence appended at seq_lens[b] (see fdi4_append_paged);
-// seq_lens is left for the caller to advance.
-void append_paged(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_stage,
-                  torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor k_scale,
-                  torch::Tensor k_zp, torch::Tensor page_table, torch::Tensor seq_lens,
-                  int64_t group_rows) {
+// seq_lens is left for the caller to advance, or, with lens_next (int32,
+// [>= batch], not seq_lens), the advanced lengths are written there
+// (fdi4_append_paged_advance).
+void append_paged_impl(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_stage,
+                       torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor k_scale,
+                       torch::Tensor k_zp, torch::Tensor page_table, torch::Tensor seq_lens,
+                       int64_t group_rows, c10::optional<torch::Tensor> lens_next) {
   CHECK_DEV(k_new);
   CHECK_DEV(v_new);
   CHECK_DEV(k_stage);
@@ -331,6 +333,21 @@ void append_paged(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_stag
   fdi4_paged_cache c = make_cache(k_pages, &v_pages, k_scale, k_zp, page_table, seq_lens,
                                   c10::nullopt, group_rows / k_pages.size(2), max_pages);
   const DeviceGuard guard(k_new.device());
+  if (lens_next) {
+    const torch::Tensor& next = *lens_next;
+    CHECK_INPUT(next);
+    CHECK_SAME_DEVICE(k_new, next);
+    TORCH_CHECK(next.scalar_type() == torch::kInt32 && next.dim() == 1 && next.size(0) >= B,
+                "lens_next must be int32 [>= batch]");
+    check_rc(fdi4_append_paged_advance(k_new.data_ptr<float>(), k_new.stride(0),
+                                       k_new.stride(1), v_new.data_ptr(), v_new.stride(0),
+                                       v_new.stride(1), (int)B, k_stage.data_ptr<float>(),
+                                       k_stage.stride(0), k_stage.stride(1), k_stage.stride(2),
+                                       (int)group_rows, &c, lens_next->data_ptr<int32_t>(),
+                                       stream()),
+             "append_paged_advance");
+    return;
+  }
   check_rc(fdi4_append_paged(k_new.data_ptr<float>(), k_new.stride(0), k_new.stride(1),
                              v_new.data_ptr(), v_new.stride(0), v_new.stride(1), (int)B,
                              k_stage.data_ptr<float>(), k_stage.stride(0), k_stage.stride(1),
@@ -338,12 +355,99 @@ void append_paged(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_stag
            "append_paged");
 }
 
-torch::Tensor decode_paged(torch::Tensor query, torch::Tensor k_pages, torch::Tensor v_pages,
-                           torch::Tensor k_scale, torch::Tensor k_zp,
-                           c10::optional<torch::Tensor> page_table,
-                           c10::optional<torch::Tensor> seq_lens,
-                           c10::optional<torch::Tensor> page_lens, int64_t pages_per_group,
-                           int64_t max_pages, int64_t num_splits) {
+// One decode step of a serving loop on the device (see fdi4_decode_step):
+// append k_new/v_new at each sequence's length, attend with query over the
+// advanced lengths, advance seq_lens. counters (int32 [>= batch], zero) and
+// lens_next (int32 [>= batch]) belong to the cache; returns [B, Hq, D] in the
+// query's dtype.
+torch::Tensor decode_step(torch::Tensor query, torch::Tensor k_new, torch::Tensor v_new,
+                          torch::Tensor k_stage, torch::Tensor k_pages, torch::Tensor v_pages,
+                          torch::Tensor k_scale, torch::Tensor k_zp, torch::Tensor page_table,
+                          torch::Tensor seq_lens, int64_t group_rows, torch::Tensor counters,
+                          torch::Tensor lens_next) {
+  CHECK_DEV(query);
+  CHECK_DEV(k_new);
+  CHECK_DEV(v_new);
+  CHECK_DEV(k_stage);
+  const int qcode = elem_code(query, "query");
+  TORCH_CHECK(query.dim() == 3 && query.stride(2) == 1,
+              "query must be [batch, heads, head_dim] with contiguous rows");
+  TORCH_CHECK(k_new.scalar_type() == torch::kFloat32 && k_new.dim() == 3 && k_new.stride(2) == 1,
+              "k_new must be float32 [batch, kv_heads, head_dim] with contiguous rows");
+  TORCH_CHECK(v_new.scalar_type() == v_pages.scalar_type() && v_new.dim() == 3 &&
+                  v_new.stride(2) == 1 && v_new.sizes() == k_new.sizes(),
+              "v_new must be [batch, kv_heads, head_dim] in the cache's value dtype");
+  TORCH_CHECK(k_stage.scalar_type() == torch::kFloat32 && k_stage.dim() == 4 &&
+                  k_stage.stride(3) == 1 && k_stage.size(2) >= group_rows,
+              "k_stage must be float32 [batch, kv_heads, >= group_rows, head_dim]");
+  TORCH_CHECK(k_new.size(1) == k_pages.size(1) && k_new.size(2) == k_pages.size(3) * 2 &&
+                  k_stage.size(1) == k_pages.size(1) && k_stage.size(3) == k_new.size(2) &&
+                  query.size(2) == k_new.size(2),
+              "k_new / k_stage / query heads and head_dim must match the cache");
+  const int64_t B = k_new.size(0);
+  TORCH_CHECK(query.size(0) == B, "query and k_new must have the same batch");
+  TORCH_CHECK(query.size(1) % k_pages.size(1) == 0,
+              "query heads must be a multiple of kv_heads");
+  TORCH_CHECK(k_stage.size(0) >= B && seq_lens.size(0) >= B && page_table.size(0) >= B &&
+                  k_scale.dim() == 4 && k_scale.size(0) >= B,
+              "k_stage, seq_lens, page_table and k_scale need a row per sequence");
+  TORCH_CHECK(group_rows % k_pages.size(2) == 0, "group_rows must be a multiple of page_rows");
+  const int64_t max_pages = page_table.size(1);
+  TORCH_CHECK(k_scale.size(2) * (group_rows / k_pages.size(2)) >= max_pages,
+              "k_scale has fewer than ceil(max_pages / pages_per_group) groups");
+  for (const torch::Tensor* t : {&counters, &lens_next}) {
+    CHECK_INPUT(*t);
+    TORCH_CHECK(t->scalar_type() == torch::kInt32 && t->dim() == 1 && t->size(0) >= B,
+                "counters and lens_next must be int32 [>= batch]");
+  }
+  CHECK_SAME_DEVICE(query, k_new);
+  CHECK_SAME_DEVICE(query, v_new);
+  CHECK_SAME_DEVICE(query, k_stage);
+  CHECK_SAME_DEVICE(query, k_pages);
+  CHECK_SAME_DEVICE(query, counters);
+  CHECK_SAME_DEVICE(query, lens_next);
+  fdi4_paged_cache c = make_cache(k_pages, &v_pages, k_scale, k_zp, page_table, seq_lens,
+                                  c10::nullopt, group_rows / k_pages.size(2), max_pages);
+  const DeviceGuard guard(query.device());
+  const int Hq = (int)query.size(1), D = (int)query.size(2);
+  auto out = torch::empty({B, Hq, D}, query.options());
+  const int splits = fdi4_decode_num_splits((int)B, Hq, &c);
+  auto ws = workspace(query, fdi4_decode_workspace_bytes((int)B, Hq, D, splits));
+  check_rc(fdi4_decode_step(query.data_ptr(), qcode, (int)B, Hq, query.stride(0),
+                            query.stride(1), k_new.data_ptr<float>(), k_new.stride(0),
+                            k_new.stride(1), v_new.data_ptr(), v_new.stride(0), v_new.stride(1),
+                            k_stage.data_ptr<float>(), k_stage.stride(0), k_stage.stride(1),
+                            k_stage.stride(2), (int)group_rows, &c, out.data_ptr(), qcode,
+                            out.stride(0), out.stride(1), counters.data_ptr<int32_t>(),
+                            lens_next.data_ptr<int32_t>(), ws.data_ptr(), ws.numel(),
+                            stream()),
+           "decode_step");
+  return out;
+}
+
+void append_paged(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_stage,
+                  torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor k_scale,
+                  torch::Tensor k_zp, torch::Tensor page_table, torch::Tensor seq_lens,
+                  int64_t group_rows) {
+  append_paged_impl(k_new, v_new, k_stage, k_pages, v_pages, k_scale, k_zp, page_table,
+                    seq_lens, group_rows, c10::nullopt);
+}
+
+void append_paged_advance(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_stage,
+                          torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor k_scale,
+                          torch::Tensor k_zp, torch::Tensor page_table, torch::Tensor seq_lens,
+                          int64_t group_rows, torch::Tensor lens_next) {
+  append_paged_impl(k_new, v_new, k_stage, k_pages, v_pages, k_scale, k_zp, page_table,
+                    seq_lens, group_rows, lens_next);
+}
+
+torch::Tensor decode_paged_impl(torch::Tensor query, torch::Tensor k_pages,
+                                torch::Tensor v_pages, torch::Tensor k_scale, torch::Tensor k_zp,
+                                c10::optional<torch::Tensor> page_table,
+                                c10::optional<torch::Tensor> seq_lens,
+                                c10::optional<torch::Tensor> page_lens, int64_t pages_per_group,
+                                int64_t max_pages, int64_t num_splits,
+                                c10::optional<torch::Tensor> lens_out) {
   CHECK_DEV(query);
   const int qcode = elem_code(query, "query");
   TORCH_CHECK(query.dim() == 3 && query.stride(2) == 1,
@@ -372,11 +476,47 @@ torch::Tensor decode_paged(torch::Tensor query, torch::Tensor k_pages, torch::Te
   auto out = torch::empty({B, Hq, D}, query.options());
   const int splits = num_splits > 0 ? (int)num_splits : fdi4_decode_num_splits(B, Hq, &c);
   auto ws = workspace(query, fdi4_decode_workspace_bytes(B, Hq, D, splits));
+  if (lens_out) {
+    const torch::Tensor& back = *lens_out;
+    CHECK_INPUT(back);
+    CHECK_SAME_DEVICE(query, back);
+    TORCH_CHECK(back.scalar_type() == torch::kInt32 && back.dim() == 1 && back.size(0) >= B,
+                "lens_out must be int32 [>= batch]");
+    TORCH_CHECK(seq_lens && seq_lens->defined(), "lens_out needs seq_lens");
+    check_rc(fdi4_decode_paged_advance(query.data_ptr(), qcode, B, Hq, query.stride(0),
+                                       query.stride(1), &c, out.data_ptr(), qcode,
+                                       out.stride(0), out.stride(1), splits, ws.data_ptr(),
+                                       ws.numel(), lens_out->data_ptr<int32_t>(), stream()),
+             "decode_paged_advance");
+    return out;
+  }
   check_rc(fdi4_decode_paged_ex(query.data_ptr(), qcode, B, Hq, query.stride(0), query.stride(1),
                                 &c, out.data_ptr(), qcode, out.stride(0), out.stride(1), splits,
                                 ws.data_ptr(), ws.numel(), stream()),
            "decode_paged");
   return out;
+}
+
+torch::Tensor decode_paged(torch::Tensor query, torch::Tensor k_pages, torch::Tensor v_pages,
+                           torch::Tensor k_scale, torch::Tensor k_zp,
+                           c10::optional<torch::Tensor> page_table,
+                           c10::optional<torch::Tensor> seq_lens,
+                           c10::optional<torch::Tensor> page_lens, int64_t pages_per_group,
+                           int64_t max_pages, int64_t num_splits) {
+  return decode_paged_impl(query, k_pages, v_pages, k_scale, k_zp, page_table, seq_lens,
+                           page_lens, pages_per_group, max_pages, num_splits, c10::nullopt);
+}
+
+// decode_paged that also copies the lengths it reads to lens_out (the
+// second launch of a serving step; see fdi4_decode_paged_advance).
+torch::Tensor decode_paged_advance(torch::Tensor query, torch::Tensor k_pages,
+                                   torch::Tensor v_pages, torch::Tensor k_scale,
+                                   torch::Tensor k_zp, c10::optional<torch::Tensor> page_table,
+                                   torch::Tensor seq_lens, int64_t pages_per_group,
+                                   int64_t max_pages, int64_t num_splits,
+                                   torch::Tensor lens_out) {
+  return decode_paged_impl(query, k_pages, v_pages, k_scale, k_zp, page_table, seq_lens,
+                           c10::nullopt, pages_per_group, max_pages, num_splits, lens_out);
 }
 
 // Decode kernel alone into a caller-provided partials buffer (uint8 tensor of
@@ -517,6 +657,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("append_paged", &append_paged,
         "Decode-time append: one token per sequence, open group re-quantized (HIP)");
   m.def("decode_paged", &decode_paged, "Split-K INT4 flash decoding over paged keys (HIP)");
+  m.def("decode_step", &decode_step,
+        "One serving step: append, decode over the advanced lengths, advance them (HIP)");
+  m.def("append_paged_advance", &append_paged_advance,
+        "Decode-time append that writes the advanced lengths to a second array (HIP)");
+  m.def("decode_paged_advance", &decode_paged_advance,
+        "decode_paged that copies the lengths it reads to a second array (HIP)");
   m.def("decode_paged_partials", &decode_paged_partials,
         "Decode kernel alone, writing split partials (HIP)");
   m.def("merge_splits", &merge_splits, "Log-sum-exp merge of split partials (HIP)");

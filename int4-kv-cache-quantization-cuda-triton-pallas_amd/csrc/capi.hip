@@ -339,11 +339,21 @@ int fdi4_quantize_paged(const float* k, int batch, int max_tokens, int64_t k_bat
                                      max_tokens, stream);
 }
 
-int fdi4_append_paged(const float* k_new, int64_t kn_batch_stride, int64_t kn_head_stride,
-                      const void* v_new, int64_t vn_batch_stride, int64_t vn_head_stride,
-                      int batch, float* k_stage, int64_t st_batch_stride, int64_t st_head_stride,
-                      int64_t st_row_stride, int group_rows, const fdi4_paged_cache* cache,
-                      hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The [0, n) int32 ranges at p and q do not overlap.
+bool disjoint_lens(const int32_t* p, const int32_t* q, int n) {
+  return p + n <= q || q + n <= p;
+}
+
+// The checks of fdi4_append_paged, and its kernel argument block.
+int make_append_args(const float* k_new, int64_t kn_batch_stride, int64_t kn_head_stride,
+                     const void* v_new, int64_t vn_batch_stride, int64_t vn_head_stride,
+                     int batch, float* k_stage, int64_t st_batch_stride, int64_t st_head_stride,
+                     int64_t st_row_stride, int group_rows, const fdi4_paged_cache* cache,
+                     fdi4::AppendArgs* out) {
   int rc = check_grouped_cache(cache, group_rows, true);
   if (rc != hipSuccess) return rc;
   if (!k_new || !v_new || !k_stage || batch < 0 || batch > 65535) return hipErrorInvalidValue;
@@ -354,7 +364,7 @@ int fdi4_append_paged(const float* k_new, int64_t kn_batch_stride, int64_t kn_he
       st_batch_stride % 4 || st_head_stride % 4 || st_row_stride % 4 || st_row_stride < D ||
       !aligned(v_new, 16) || (vn_batch_stride * veb) % 16 || (vn_head_stride * veb) % 16)
     return hipErrorInvalidValue;
-  fdi4::AppendArgs a;
+  fdi4::AppendArgs& a = *out;
   a.q = quant_args(cache);
   a.q.k = nullptr;
   a.q.k_b = a.q.k_h = a.q.k_t = 0;
@@ -375,7 +385,52 @@ int fdi4_append_paged(const float* k_new, int64_t kn_batch_stride, int64_t kn_he
   a.st_h = st_head_stride;
   a.st_r = st_row_stride;
   a.capacity = cache->max_pages * cache->page_rows;
-  return fdi4::launch_append_paged(a, D, group_rows, batch, cache->num_kv_heads, stream);
+  a.lens_next = nullptr;
+  return hipSuccess;
+}
+
+int append_paged_any(const float* k_new, int64_t kn_batch_stride, int64_t kn_head_stride,
+                     const void* v_new, int64_t vn_batch_stride, int64_t vn_head_stride,
+                     int batch, float* k_stage, int64_t st_batch_stride, int64_t st_head_stride,
+                     int64_t st_row_stride, int group_rows, const fdi4_paged_cache* cache,
+                     int32_t* lens_next, hipStream_t stream) {
+  fdi4::AppendArgs a;
+  const int rc = make_append_args(k_new, kn_batch_stride, kn_head_stride, v_new, vn_batch_stride,
+                                  vn_head_stride, batch, k_stage, st_batch_stride,
+                                  st_head_stride, st_row_stride, group_rows, cache, &a);
+  if (rc != hipSuccess) return rc;
+  a.lens_next = lens_next;
+  return fdi4::launch_append_paged(a, cache->head_dim, group_rows, batch, cache->num_kv_heads,
+                                   stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int fdi4_append_paged(const float* k_new, int64_t kn_batch_stride, int64_t kn_head_stride,
+                      const void* v_new, int64_t vn_batch_stride, int64_t vn_head_stride,
+                      int batch, float* k_stage, int64_t st_batch_stride, int64_t st_head_stride,
+                      int64_t st_row_stride, int group_rows, const fdi4_paged_cache* cache,
+                      hipStream_t stream) {
+  return append_paged_any(k_new, kn_batch_stride, kn_head_stride, v_new, vn_batch_stride,
+                          vn_head_stride, batch, k_stage, st_batch_stride, st_head_stride,
+                          st_row_stride, group_rows, cache, nullptr, stream);
+}
+
+int fdi4_append_paged_advance(const float* k_new, int64_t kn_batch_stride,
+                              int64_t kn_head_stride, const void* v_new,
+                              int64_t vn_batch_stride, int64_t vn_head_stride, int batch,
+                              float* k_stage, int64_t st_batch_stride, int64_t st_head_stride,
+                              int64_t st_row_stride, int group_rows,
+                              const fdi4_paged_cache* cache, int32_t* lens_next,
+                              hipStream_t stream) {
+  if (!cache || !cache->seq_lens || !lens_next || !aligned(lens_next, 4) || batch < 0 ||
+      !disjoint_lens(lens_next, cache->seq_lens, batch))
+    return hipErrorInvalidValue;
+  return append_paged_any(k_new, kn_batch_stride, kn_head_stride, v_new, vn_batch_stride,
+                          vn_head_stride, batch, k_stage, st_batch_stride, st_head_stride,
+                          st_row_stride, group_rows, cache, lens_next, stream);
 }
 
 int fdi4_decode_num_splits(int batch, int num_q_heads, const fdi4_paged_cache* cache) {
@@ -480,6 +535,8 @@ int make_decode_args(const void* query, int q_dtype, int batch, int num_q_heads,
   a->waves = plan.waves;
   a->heads_per_wg = plan.heads_per_wg;
   a->mfma = plan.mfma;
+  a->lens_out = nullptr;
+  a->step = fdi4::StepAppend{};
   return hipSuccess;
 }
 
@@ -503,11 +560,13 @@ int decode_paged_any(const void* query, int q_dtype, int batch, int num_q_heads,
                      int64_t q_batch_stride, int64_t q_head_stride,
                      const fdi4_paged_cache* cache, void* out, int out_dtype,
                      int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
-                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                     void* workspace, size_t workspace_bytes, int32_t* lens_out,
+                     hipStream_t stream) {
   DecodeArgs a;
   int rc = make_decode_args(query, q_dtype, batch, num_q_heads, q_batch_stride, q_head_stride,
                             cache, num_splits, &a);
   if (rc != hipSuccess) return rc;
+  a.lens_out = lens_out;
   if (!out || !valid_elem_dtype(out_dtype)) return hipErrorInvalidValue;
   const int d = cache->head_dim;
   a.out = out;
@@ -536,7 +595,7 @@ int fdi4_decode_paged(const float* query, int batch, int num_q_heads, int64_t q_
                       void* workspace, size_t workspace_bytes, hipStream_t stream) {
   return decode_paged_any(query, FDI4_K_F32, batch, num_q_heads, q_batch_stride, q_head_stride,
                           cache, out, FDI4_K_F32, out_batch_stride, out_head_stride, num_splits,
-                          workspace, workspace_bytes, stream);
+                          workspace, workspace_bytes, nullptr, stream);
 }
 
 int fdi4_decode_paged_ex(const void* query, int query_dtype, int batch, int num_q_heads,
@@ -546,7 +605,83 @@ int fdi4_decode_paged_ex(const void* query, int query_dtype, int batch, int num_
                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
   return decode_paged_any(query, query_dtype, batch, num_q_heads, q_batch_stride, q_head_stride,
                           cache, out, out_dtype, out_batch_stride, out_head_stride, num_splits,
-                          workspace, workspace_bytes, stream);
+                          workspace, workspace_bytes, nullptr, stream);
+}
+
+int fdi4_decode_paged_advance(const void* query, int query_dtype, int batch, int num_q_heads,
+                              int64_t q_batch_stride, int64_t q_head_stride,
+                              const fdi4_paged_cache* cache, void* out, int out_dtype,
+                              int64_t out_batch_stride, int64_t out_head_stride, int num_splits,
+                              void* workspace, size_t workspace_bytes, int32_t* lens_out,
+                              hipStream_t stream) {
+  if (!cache || !cache->seq_lens || !lens_out || !aligned(lens_out, 4) || batch < 0 ||
+      !disjoint_lens(lens_out, cache->seq_lens, batch))
+    return hipErrorInvalidValue;
+  return decode_paged_any(query, query_dtype, batch, num_q_heads, q_batch_stride, q_head_stride,
+                          cache, out, out_dtype, out_batch_stride, out_head_stride, num_splits,
+                          workspace, workspace_bytes, lens_out, stream);
+}
+
+int fdi4_decode_step(const void* query, int query_dtype, int batch, int num_q_heads,
+                     int64_t q_batch_stride, int64_t q_head_stride, const float* k_new,
+                     int64_t kn_batch_stride, int64_t kn_head_stride, const void* v_new,
+                     int64_t vn_batch_stride, int64_t vn_head_stride, float* k_stage,
+                     int64_t st_batch_stride, int64_t st_head_stride, int64_t st_row_stride,
+                     int group_rows, const fdi4_paged_cache* cache, void* out, int out_dtype,
+                     int64_t out_batch_stride, int64_t out_head_stride, int32_t* counters,
+                     int32_t* lens_next, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+  fdi4::AppendArgs ap;
+  int rc = make_append_args(k_new, kn_batch_stride, kn_head_stride, v_new, vn_batch_stride,
+                            vn_head_stride, batch, k_stage, st_batch_stride, st_head_stride,
+                            st_row_stride, group_rows, cache, &ap);
+  if (rc != hipSuccess) return rc;
+  const int32_t* lens = cache->seq_lens;
+  if (!counters || !lens_next || !aligned(counters, 4) || !aligned(lens_next, 4) ||
+      !disjoint_lens(counters, lens, batch) || !disjoint_lens(lens_next, lens, batch) ||
+      !disjoint_lens(counters, lens_next, batch))
+    return hipErrorInvalidValue;
+  DecodeArgs a;
+  rc = make_decode_args(query, query_dtype, batch, num_q_heads, q_batch_stride, q_head_stride,
+                        cache, 0, &a);
+  if (rc != hipSuccess) return rc;
+  if (!out || !valid_elem_dtype(out_dtype)) return hipErrorInvalidValue;
+  // One workgroup per (sequence, kv-head): the append fuses into the decode.
+  const bool fused = a.num_splits == 1 && !a.mfma && a.heads_per_wg == 1 && a.hq_per_kv == 1;
+  if (!fused) {
+    // Two launches: the append writes the advanced lengths to lens_next, the
+    // decode attends over them and copies them back to the cache's lengths.
+    ap.lens_next = lens_next;
+    hipError_t e = fdi4::launch_append_paged(ap, cache->head_dim, group_rows, batch,
+                                             cache->num_kv_heads, stream);
+    if (e != hipSuccess) return e;
+    fdi4_paged_cache next = *cache;
+    next.seq_lens = lens_next;
+    return decode_paged_any(query, query_dtype, batch, num_q_heads, q_batch_stride,
+                            q_head_stride, &next, out, out_dtype, out_batch_stride,
+                            out_head_stride, 0, workspace, workspace_bytes,
+                            const_cast<int32_t*>(lens), stream);
+  }
+  a.out = out;
+  a.out_dtype = out_dtype;
+  a.o_b = out_batch_stride;
+  a.o_h = out_head_stride;
+  a.final_out = 1;
+  fdi4::StepAppend& st = a.step;
+  st.k_new = k_new;
+  st.kn_b = ap.kn_b;
+  st.kn_h = ap.kn_h;
+  st.v_new = ap.v_new;
+  st.vn_b = ap.vn_b;
+  st.vn_h = ap.vn_h;
+  st.stage = k_stage;
+  st.st_b = st_batch_stride;
+  st.st_h = st_head_stride;
+  st.st_r = st_row_stride;
+  st.group_rows = group_rows;
+  st.arrive = counters;
+  st.lens = const_cast<int32_t*>(lens);
+  return fdi4::launch_decode(a, cache->head_dim, cache->v_dtype, batch, stream);
 }
 
 int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,

@@ -32,7 +32,10 @@
 //   valid count are loaded from the last valid row (never out of bounds) and
 //   masked to probability 0.
 
+#include <limits.h>
+
 #include "decode_common.hpp"
+#include "quant_common.hpp"
 
 namespace fdi4 {
 
@@ -54,7 +57,36 @@ struct Geo {
   static_assert(RPL >= 1 && 16 % RPL == 0 && 16 % TPW == 0, "geometry");
 };
 
-template <int D, int VDT, int WAVES>
+// The fused serving step's append (STEP instantiations): this workgroup
+// writes token t of its (sequence, kv-head) and re-quantizes the open group
+// (step_requant).
+template <int D, int NT, int VEB>
+__device__ __forceinline__ void step_append(const DecodeArgs& a, int b, int hk, int t) {
+  step_requant<D, NT, VEB>(a.step, const_cast<uint8_t*>(a.k_pages), a.k_page, a.k_head, a.k_row,
+                           reinterpret_cast<uint8_t*>(const_cast<void*>(a.v_pages)),
+                           a.v_page * VEB, a.v_head * VEB, a.v_row * VEB,
+                           const_cast<float*>(a.k_scale), const_cast<float*>(a.k_zp), a.s_b,
+                           a.s_h, a.s_g, a.page_table, a.pt_b, a.page_rows, a.num_pages, b, hk,
+                           t);
+}
+
+// The fused serving step's length advance: every workgroup of sequence b
+// counts its arrival when it has finished (each read the old length at its
+// start); the last to arrive writes the new length and clears the counter for
+// the next step. A relaxed device-scope atomic: the count is all the
+// arrivals need to agree on.
+__device__ __forceinline__ void step_arrive(const DecodeArgs& a, int b, int T) {
+  if (threadIdx.x != 0) return;
+  const int n = gridDim.x * gridDim.y;
+  const int prev =
+      __hip_atomic_fetch_add(a.step.arrive + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (prev == n - 1) {
+    __hip_atomic_store(a.step.arrive + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    a.step.lens[b] = T;
+  }
+}
+
+template <int D, int VDT, int WAVES, bool STEP>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   using G = Geo<D, VDT>;
   constexpr int NT = WAVES * 64;
@@ -78,7 +110,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   __shared__ float l_s[WAVES];
 
   const int cpp = (a.page_rows + 15) >> 4;
-  const int T = seq_len_of(a, b);
+  // With STEP, token t_app = seq_lens[b] is appended (none when the sequence
+  // already fills the cache) and the decode attends over t_app + 1 rows.
+  int T, t_app = -1;
+  if constexpr (STEP) {
+    const int cap = a.max_pages * a.page_rows;
+    const int t = min(max(ld_ro(a.seq_lens, b), 0), cap);
+    t_app = t < cap ? t : -1;
+    T = t_app >= 0 ? t + 1 : t;
+  } else {
+    T = seq_len_of(a, b);
+  }
   const int n_chunks = pages_of(a, T) * cpp;
   const int c_begin = split * a.chunks_per_split;
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
@@ -252,9 +294,26 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   const bool has_work = c < wc1;
   KVec<G::KW> ka[G::KLD], kb[G::KLD];
   U32x4 va[G::VLD], vb[G::VLD];
+  // With STEP the first chunk's loads go out before the append when the chunk
+  // lies before the open group (first chunk og_first), so its latency
+  // overlaps the re-quantization; a chunk of the open group is loaded after.
+  int og_first = INT_MAX;
+  if constexpr (STEP) {
+    if (t_app >= 0) og_first = (t_app / a.step.group_rows) * a.step.group_rows / a.page_rows * cpp;
+  }
+  const bool early = has_work && wr.chunk_at(c) < og_first;
   if (has_work) {
     cm = meta_at(c);
     nm = meta_at(c + 1);
+  }
+  if (early) {
+    load_sz(cm, sz);
+    load_chunk(cm, ka, va);
+  }
+  if constexpr (STEP) {
+    if (t_app >= 0) step_append<D, NT, G::VEB>(a, b, hk, t_app);
+  }
+  if (has_work && !early) {
     load_sz(cm, sz);
     load_chunk(cm, ka, va);
   }
@@ -307,6 +366,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     a.ws_ml[2 * pi] = ms;
     a.ws_ml[2 * pi + 1] = (double)l;
   }
+  hand_back_length(a, b);
+  if constexpr (STEP) step_arrive(a, b, T);
 }
 
 // Log-sum-exp merge of the split partials: grid (Hq, B), one thread per channel.
@@ -334,7 +395,10 @@ hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hip
   dim3 grid(a.num_splits, a.num_q_heads, batch);
 #define FDI4_DEC(DD, VV, WW)                                                             \
   if (D == DD && v_dtype == VV && a.waves == WW) {                                       \
-    hipLaunchKernelGGL((decode_kernel<DD, VV, WW>), grid, dim3(WW * 64), 0, st, a);      \
+    if (a.step.k_new)                                                                    \
+      hipLaunchKernelGGL((decode_kernel<DD, VV, WW, true>), grid, dim3(WW * 64), 0, st, a); \
+    else                                                                                 \
+      hipLaunchKernelGGL((decode_kernel<DD, VV, WW, false>), grid, dim3(WW * 64), 0, st, a); \
     return hipGetLastError();                                                            \
   }
   FDI4_DEC(64, kVF32, 4) FDI4_DEC(128, kVF32, 4) FDI4_DEC(256, kVF32, 4)

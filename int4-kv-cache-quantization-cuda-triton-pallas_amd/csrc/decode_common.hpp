@@ -78,6 +78,16 @@ __device__ __forceinline__ void widen_values(const U32x4& v, float* f) {
   }
 }
 
+// Element i of a read-only int32 kernel input (page table, page lengths,
+// sequence lengths) through the constant address space: at a wave-uniform
+// index a scalar-unit load, also in a kernel that stores to the cache before
+// its chunk loop (the fused serving step), where the compiler would otherwise
+// treat the arrays as possibly overwritten and load them as vectors, each
+// load followed by a full vmcnt drain.
+__device__ __forceinline__ int ld_ro(const int32_t* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
+}
+
 struct ChunkMeta {
   int64_t phys;
   int r0;
@@ -92,13 +102,13 @@ __device__ __forceinline__ ChunkMeta chunk_meta(const DecodeArgs& a, int b, int 
   const int j = c - lp * cpp;
   int rows;
   if (a.page_lens) {
-    rows = min(max(a.page_lens[(int64_t)b * a.pl_b + lp], 0), a.page_rows);
+    rows = min(max(ld_ro(a.page_lens, (int64_t)b * a.pl_b + lp), 0), a.page_rows);
   } else {
     rows = min(a.page_rows, T - lp * a.page_rows);
   }
   m.r0 = j * 16;
   m.nval = min(16, rows - m.r0);
-  const int pg = a.page_table ? a.page_table[(int64_t)b * a.pt_b + lp] : lp;
+  const int pg = a.page_table ? ld_ro(a.page_table, (int64_t)b * a.pt_b + lp) : lp;
   m.phys = (int64_t)min(max(pg, 0), a.num_pages - 1);
   m.group = lp / a.pages_per_group;
   return m;
@@ -110,7 +120,18 @@ __device__ __forceinline__ ChunkMeta chunk_meta(const DecodeArgs& a, int b, int 
 // no lengths are given.
 __device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
   const int cap = a.max_pages * a.page_rows;
-  return a.seq_lens ? min(max(a.seq_lens[b], 0), cap) : cap;
+  return a.seq_lens ? min(max(ld_ro(a.seq_lens, b), 0), cap) : cap;
+}
+
+// The serving step's length hand-back, at the end of the decode: workgroup
+// (split 0, first head group) of sequence b copies the length it read to
+// lens_out[b]. No workgroup of the decode reads lens_out, a different array
+// from seq_lens (the host checks both). (At the start of the kernel the
+// store would make the compiler treat the page-table reads of the chunk loop
+// as possibly clobbered and turn them into vector loads.)
+__device__ __forceinline__ void hand_back_length(const DecodeArgs& a, int b) {
+  if (a.lens_out && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+    a.lens_out[b] = a.seq_lens[b];
 }
 
 // Logical pages holding the first T rows (T <= max_pages * page_rows).

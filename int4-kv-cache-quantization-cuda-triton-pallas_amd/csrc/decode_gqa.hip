@@ -350,6 +350,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gqa_kernel(DecodeArgs a) {
       }
     }
   }
+  hand_back_length(a, b);
 }
 
 hipError_t launch_decode_gqa(const DecodeArgs& a, int D, int v_dtype, int batch, int hg,

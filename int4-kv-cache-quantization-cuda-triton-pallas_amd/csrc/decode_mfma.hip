@@ -389,6 +389,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
       }
     }
   }
+  hand_back_length(a, b);
 }
 
 hipError_t launch_decode_mfma(const DecodeArgs& a, int D, int v_dtype, int batch, int hg,

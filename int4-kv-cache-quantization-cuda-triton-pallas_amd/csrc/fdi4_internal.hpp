@@ -45,6 +45,23 @@ struct AppendArgs {
   float* stage;
   int64_t st_b, st_h, st_r;             // elements
   int capacity;                         // max_pages * page_rows
+  int32_t* lens_next;                   // null, or [B]: the length after this append
+};
+
+// Where the fused serving step of the decode writes one token (k_new null:
+// no step): the new key row (float32),
+// the new value row (the cache's value type, as bytes) and the staging rows
+// of the open group, per (sequence, kv-head).
+struct StepAppend {
+  const float* k_new;
+  int64_t kn_b, kn_h;                   // elements
+  const uint8_t* v_new;
+  int64_t vn_b, vn_h;                   // bytes
+  float* stage;
+  int64_t st_b, st_h, st_r;             // elements
+  int group_rows;                       // 64, 128 or 256, a multiple of page_rows
+  int32_t* arrive;                      // [B] arrival counters, zero between steps
+  int32_t* lens;                        // [B] the lengths, advanced by the last arriver
 };
 
 // Split-K paged decode.
@@ -75,6 +92,8 @@ struct DecodeArgs {
   int64_t o_b, o_h;
   float* ws_acc;                        // [B, Hq, S, D]
   double* ws_ml;                        // [B, Hq, S, 2] = (m, l)
+  int32_t* lens_out;                    // null, or [B]: receives the lengths read
+  StepAppend step;                      // the fused serving step (step.k_new != null)
 };
 
 // Quantize-dequantize of keys [B, H, T, D] (channel stride 1) in blocks of

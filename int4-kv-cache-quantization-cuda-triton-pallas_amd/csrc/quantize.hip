@@ -29,39 +29,14 @@
 //       token at position seq_lens[b] (value row to its page, key row to the
 //       staging rows of the open group) and re-quantizes that group over its
 //       valid rows, exactly what the grouped quantizer gives for the whole
-//       sequence.
+//       sequence; optionally writes the advanced length to a second array.
 //   pack_kernel   device form of the nibble packing (reference src/int4_pack.py:14-29)
 
 #include "fdi4_device.hpp"
 #include "fdi4_internal.hpp"
+#include "quant_common.hpp"
 
 namespace fdi4 {
-
-__device__ __forceinline__ unsigned quant_bin(float x, float mn, float scale) {
-  float b = rintf((x - mn) / scale);
-  b = fminf(fmaxf(b, 0.0f), 15.0f);
-  return (unsigned)b;
-}
-
-// The same bin with the division done from the reciprocal rc = 1.0f / scale
-// (one IEEE division per channel): q0 = y * rc, then one FMA residual step
-// q = fma(fma(-q0, scale, y), rc, q0) yields the correctly rounded quotient
-// RN(y / scale) (Markstein's correction: rc is the correctly rounded
-// reciprocal, the residual y - q0 * scale is exact under FMA, and no
-// intermediate under- or overflows for 0 <= y <= span and scale >= 1e-8/15).
-// Infinite or NaN inputs give a NaN quotient and bin 0, as the division does.
-__device__ __forceinline__ float quant_bin_rc(float x, float mn, float scale, float rc) {
-  const float y = x - mn;
-  const float q0 = y * rc;
-  const float q = __builtin_fmaf(__builtin_fmaf(-q0, scale, y), rc, q0);
-  return fminf(fmaxf(rintf(q), 0.0f), 15.0f);
-}
-
-__device__ __forceinline__ void scale_zp(float mn, float mx, float* s, float* z) {
-  const float span = fmaxf(mx - mn, 1e-8f);
-  *s = span / 15.0f;
-  *z = (-mn) / *s;
-}
 
 // ---------------------------------------------------------------------------
 // 2-D contract: [rows, C] row-major, one group over all rows.
@@ -759,7 +734,12 @@ __global__ __launch_bounds__(kQThreads) void append_paged_kernel(AppendArgs a) {
   using G = QGeo<D, GROUP>;
   const int h = blockIdx.x, b = blockIdx.y;
   const int t = a.q.seq_lens[b];
-  if (t < 0 || t >= a.capacity) return;
+  const bool fits = t >= 0 && t < a.capacity;
+  // The serving step's length advance: one workgroup per sequence writes the
+  // length after this append to a separate array (no workgroup of this
+  // kernel reads it, so the other heads of the sequence still read t).
+  if (a.lens_next && h == 0 && threadIdx.x == 0) a.lens_next[b] = fits ? t + 1 : t;
+  if (!fits) return;
   const int g = t / GROUP, rnew = t % GROUP;
   const int tid = threadIdx.x;
   const int cq = tid % G::VPR, rsub = tid / G::VPR;

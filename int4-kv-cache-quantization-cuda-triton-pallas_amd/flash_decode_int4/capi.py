@@ -68,6 +68,10 @@ SIGNATURES = {
     "fdi4_append_paged": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int,
                                   c_void_p, c_int64, c_int64, c_int64, c_int,
                                   ctypes.POINTER(PagedCache), c_void_p]),
+    "fdi4_append_paged_advance": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64,
+                                          c_int64, c_int, c_void_p, c_int64, c_int64, c_int64,
+                                          c_int, ctypes.POINTER(PagedCache), c_void_p,
+                                          c_void_p]),
     "fdi4_flash_decode_int4": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
                                        c_void_p]),
@@ -83,6 +87,15 @@ SIGNATURES = {
     "fdi4_decode_paged_ex": (c_int, [c_void_p, c_int, c_int, c_int, c_int64, c_int64,
                                      ctypes.POINTER(PagedCache), c_void_p, c_int, c_int64,
                                      c_int64, c_int, c_void_p, c_size_t, c_void_p]),
+    "fdi4_decode_paged_advance": (c_int, [c_void_p, c_int, c_int, c_int, c_int64, c_int64,
+                                          ctypes.POINTER(PagedCache), c_void_p, c_int, c_int64,
+                                          c_int64, c_int, c_void_p, c_size_t, c_void_p,
+                                          c_void_p]),
+    "fdi4_decode_step": (c_int, [c_void_p, c_int, c_int, c_int, c_int64, c_int64, c_void_p,
+                                 c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64,
+                                 c_int64, c_int64, c_int, ctypes.POINTER(PagedCache), c_void_p,
+                                 c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t,
+                                 c_void_p]),
     "fdi4_decode_partials_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "fdi4_decode_paged_partials": (c_int, [c_void_p, c_int, c_int, c_int64, c_int64,
                                            ctypes.POINTER(PagedCache), c_int, c_void_p,

@@ -206,6 +206,10 @@ class INT4PagedSequenceCache:
         self.page_table = torch.zeros(max_seqs, self.max_pages_per_seq, dtype=torch.int32,
                                       device=dev)
         self.seq_lens = torch.zeros(max_seqs, dtype=torch.int32, device=dev)
+        # step(): per-sequence arrival counters of the one-launch step (zero
+        # between steps) and the advanced lengths of the two-launch step.
+        self._step_counters = torch.zeros(max_seqs, dtype=torch.int32, device=dev)
+        self._lens_next = torch.zeros(max_seqs, dtype=torch.int32, device=dev)
         self.k_stage = torch.zeros(max_seqs, H, group_rows, D, dtype=torch.float32, device=dev)
         self._free = list(range(num_pages - 1, -1, -1))
         self._pages = [[] for _ in range(max_seqs)]
@@ -392,12 +396,27 @@ class INT4PagedSequenceCache:
         if len(short):
             raise RuntimeError(f"step() would write past the pages reserved for sequence "
                                f"{int(short[0])}; call reserve() first")
-        load_binding().append_paged(k_new, v_new, self.k_stage[:B], self.k_pages,
-                                    self.v_pages, self.k_scale[:B], self.k_zp[:B],
-                                    self.page_table[:B], self.seq_lens[:B], self.group_rows)
-        self.seq_lens[:B] += 1
         self._unsynced_steps += 1
-        return self.decode(query, num_splits)
+        if num_splits:
+            # An explicit split count: the two-launch form (the append writes
+            # seq_lens + 1 to _lens_next, the decode attends over it with the
+            # given splits and copies it back to seq_lens when it ends).
+            C = load_binding()
+            C.append_paged_advance(k_new, v_new, self.k_stage[:B], self.k_pages, self.v_pages,
+                                   self.k_scale[:B], self.k_zp[:B], self.page_table[:B],
+                                   self.seq_lens[:B], self.group_rows, self._lens_next[:B])
+            return C.decode_paged_advance(query, self.k_pages, self.v_pages, self.k_scale[:B],
+                                          self.k_zp[:B], self.page_table[:B],
+                                          self._lens_next[:B],
+                                          self.group_rows // self.page_rows,
+                                          self.max_pages_per_seq, int(num_splits),
+                                          self.seq_lens[:B])
+        # One launch when each (sequence, kv-head) is one decode workgroup,
+        # two otherwise (fdi4_decode_step decides).
+        return load_binding().decode_step(query, k_new, v_new, self.k_stage, self.k_pages,
+                                          self.v_pages, self.k_scale, self.k_zp,
+                                          self.page_table, self.seq_lens, self.group_rows,
+                                          self._step_counters, self._lens_next)
 
     def sync_lengths(self) -> None:
         """Refresh the host copy of the lengths from the device (after step())."""

@@ -175,3 +175,59 @@ def test_partials_then_merge_equals_one_call():
         merged = C.merge_splits(parts, 2, 4, 128, S)
         one = ops.flash_decode_paged(q, kp, v, s, z, pt, sl, num_splits=S)
         assert (merged - one).abs().max().item() < 1e-6, S
+
+
+def test_advance_pair_through_ctypes():
+    """fdi4_append_paged_advance then fdi4_decode_paged_advance with raw device
+    pointers: lens_next holds the advanced lengths after the append, the
+    cache's lengths are unchanged until the decode copies them back, and the
+    output equals the workspace decode over the advanced lengths."""
+    import torch
+    from flash_decode_int4 import capi
+    from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
+    lib = capi.load()
+    B, H, D = 2, 4, 128
+    c = INT4PagedSequenceCache(num_pages=64, num_kv_heads=H, head_dim=D, max_seqs=B,
+                               max_seq_len=512)
+    g = torch.Generator(device="cuda").manual_seed(21)
+    k = torch.randn(B, H, 300, D, device="cuda", generator=g)
+    c.prefill(k, torch.randn_like(k), [300, 127])
+    c.reserve(B, 1)
+    kn = torch.randn(B, H, D, device="cuda", generator=g)
+    vn = torch.randn(B, H, D, device="cuda", generator=g)
+    q = torch.randn(B, H, D, device="cuda", generator=g)
+    nxt = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+    kp, v, s = c.k_pages, c.v_pages, c.k_scale
+
+    def cache_desc(lens):
+        return capi.PagedCache(
+            k_pages=kp.data_ptr(), k_page_stride=kp.stride(0), k_head_stride=kp.stride(1),
+            k_row_stride=kp.stride(2), v_pages=v.data_ptr(), v_dtype=capi.V_F32,
+            v_page_stride=v.stride(0), v_head_stride=v.stride(1), v_row_stride=v.stride(2),
+            k_scale=s.data_ptr(), k_zp=c.k_zp.data_ptr(), s_batch_stride=s.stride(0),
+            s_head_stride=s.stride(1), s_group_stride=s.stride(2), s_page_stride=0,
+            page_table=c.page_table.data_ptr(), pt_batch_stride=c.page_table.stride(0),
+            seq_lens=lens.data_ptr(), page_lens=None, pl_batch_stride=0, num_kv_heads=H,
+            head_dim=D, page_rows=16, pages_per_group=8, max_pages=c.page_table.shape[1],
+            num_pages=kp.shape[0])
+
+    st = c.k_stage
+    capi.check(lib.fdi4_append_paged_advance(
+        _ptr(kn), kn.stride(0), kn.stride(1), _ptr(vn), vn.stride(0), vn.stride(1), B, _ptr(st),
+        st.stride(0), st.stride(1), st.stride(2), 128, cache_desc(c.seq_lens), _ptr(nxt),
+        _stream()), "append_paged_advance")
+    torch.cuda.synchronize()
+    assert nxt.tolist() == [301, 128] and c.seq_lens[:B].tolist() == [300, 127]
+    out = torch.empty(B, H, D, device="cuda")
+    ref = torch.empty(B, H, D, device="cuda")
+    capi.check(lib.fdi4_decode_paged_advance(
+        _ptr(q), capi.K_F32, B, H, q.stride(0), q.stride(1), cache_desc(nxt), _ptr(out),
+        capi.K_F32, out.stride(0), out.stride(1), 1, None, 0, _ptr(c.seq_lens), _stream()),
+        "decode_paged_advance")
+    torch.cuda.synchronize()
+    assert c.seq_lens[:B].tolist() == [301, 128]
+    capi.check(lib.fdi4_decode_paged_ex(
+        _ptr(q), capi.K_F32, B, H, q.stride(0), q.stride(1), cache_desc(c.seq_lens), _ptr(ref),
+        capi.K_F32, ref.stride(0), ref.stride(1), 1, None, 0, _stream()), "decode_paged_ex")
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)

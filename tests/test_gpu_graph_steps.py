@@ -100,3 +100,76 @@ def test_graph_replayed_steps_equal_eager_steps(value_dtype, q_heads, steps, q_d
     assert torch.equal(eager_out[steps], full.to(qdt))
     got = full.cpu().numpy()
     assert np.abs(got - o32).max() <= max(TOL, 1.25 * np.abs(o32 - o64).max())
+
+
+@pytest.mark.parametrize("q_heads,num_splits", [(4, 0), (8, 3), (16, 1)])
+def test_step_equals_append_increment_decode(q_heads, num_splits):
+    """step() (two launches: the append writes the advanced lengths to a
+    second array, the decode reads them and writes them back) against the
+    three-launch form (append, a separate length increment, decode): the same
+    outputs, pages, scales, staging rows and lengths, bit for bit, over steps
+    that cross a page and a group boundary, with one and several splits and
+    the per-head, grouped and matrix-core kernels."""
+    import torch
+    from flash_decode_int4._lib import load_binding
+    C = load_binding()
+    B, H, D = 3, 4, 128
+    lens0 = [126, 15, 250]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    k = torch.randn(B, H, 256, D, device="cuda", generator=g)
+    v = torch.randn(B, H, 256, D, device="cuda", generator=g)
+    new, old = _cache("float32"), _cache("float32")
+    for c in (new, old):
+        c.prefill(k, v, lens0)
+        c.reserve(B, 8)
+    for i in range(5):
+        kn = torch.randn(B, H, D, device="cuda", generator=g)
+        vn = torch.randn(B, H, D, device="cuda", generator=g)
+        q = torch.randn(B, q_heads, D, device="cuda", generator=g)
+        out_new = new.step(kn, vn, q, num_splits)
+        C.append_paged(kn, vn, old.k_stage[:B], old.k_pages, old.v_pages, old.k_scale[:B],
+                       old.k_zp[:B], old.page_table[:B], old.seq_lens[:B], old.group_rows)
+        old.seq_lens[:B] += 1
+        out_old = old.decode(q, num_splits)
+        torch.cuda.synchronize()
+        assert torch.equal(out_new, out_old), i
+        for name in ("k_pages", "v_pages", "k_scale", "k_zp", "seq_lens", "k_stage"):
+            assert torch.equal(getattr(new, name), getattr(old, name)), (i, name)
+    new.sync_lengths()
+    assert list(new.lengths()[:B]) == [n + 5 for n in lens0]
+
+
+def test_graph_of_several_steps_equals_eager_steps():
+    """Four steps captured in one graph, replayed twice: the outputs of the
+    last step of each replay and the final cache equal eight eager steps."""
+    import torch
+    B, H, D = 3, 4, 128
+    lens0 = [60, 128, 9]
+    g = torch.Generator(device="cuda").manual_seed(13)
+    k = torch.randn(B, H, 200, D, device="cuda", generator=g)
+    v = torch.randn(B, H, 200, D, device="cuda", generator=g)
+    eager, graphed = _cache("float32"), _cache("float32")
+    for c in (eager, graphed):
+        c.prefill(k, v, lens0)
+        c.reserve(B, 9)
+    kn = torch.randn(B, H, D, device="cuda", generator=g)
+    vn = torch.randn(B, H, D, device="cuda", generator=g)
+    q = torch.randn(B, 8, D, device="cuda", generator=g)
+    eager.step(kn, vn, q)
+    graphed.step(kn, vn, q)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(4):
+            out_g = graphed.step(kn, vn, q)
+    for r in range(2):
+        for _ in range(4):
+            out_e = eager.step(kn, vn, q)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), r
+    for name in ("k_pages", "v_pages", "k_scale", "k_zp", "seq_lens", "k_stage"):
+        assert torch.equal(getattr(graphed, name), getattr(eager, name)), name
+    graphed.sync_lengths()
+    assert list(graphed.lengths()[:B]) == [n + 9 for n in lens0]

@@ -395,6 +395,22 @@ def check_invalid_arguments_are_rejected():
                            v_pages=256, v_dtype=capi.V_F32, v_page_stride=1 << 20,
                            v_head_stride=1 << 12, v_row_stride=256, s_batch_stride=1 << 17,
                            s_head_stride=1 << 11, s_group_stride=256, seq_lens=256)
+    # The serving-step pair: the second lengths array must be given, must not
+    # overlap the cache's lengths, and the cache must carry lengths.
+    ok = capi.PagedCache(head_dim=128, page_rows=16, num_kv_heads=1, pages_per_group=8,
+                         max_pages=8, num_pages=8, k_pages=256, k_scale=256, k_zp=256,
+                         k_page_stride=1024, k_row_stride=64, v_pages=256, v_dtype=capi.V_F32,
+                         v_page_stride=2048, v_row_stride=128, s_group_stride=128,
+                         seq_lens=1024)
+    for lens_other in (None, 1024, 1028, 1020):   # missing, same array, overlapping
+        assert lib.fdi4_decode_paged_advance(q, 0, 2, 1, 128, 128, ctypes.byref(ok), q, 0, 128,
+                                             128, 1, None, 0, lens_other, None) == bad
+        assert lib.fdi4_append_paged_advance(q, 128, 128, q, 128, 128, 2, q, 1 << 14, 1 << 14,
+                                             128, 128, ctypes.byref(ok), lens_other,
+                                             None) == bad
+    ok.seq_lens = None
+    assert lib.fdi4_decode_paged_advance(q, 0, 2, 1, 128, 128, ctypes.byref(ok), q, 0, 128,
+                                         128, 1, None, 0, 4096, None) == bad
     assert lib.fdi4_decode_workspace_bytes(64, 64, 256, 2) > capi.NOALLOC_SCRATCH_BYTES
     assert lib.fdi4_decode_paged_noalloc(q, 64, 64, 1 << 14, 256, ctypes.byref(wide), q,
                                          1 << 14, 256, 2, None) == bad
