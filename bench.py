@@ -59,9 +59,10 @@ and the + 1 lengths in alternating blocks, so the two figures share clocks
 and memory state.
 
 Prints ONE JSON line. Options: --workload (anchor, sweep_512 ... llama,
-ragged), --splits, --value-dtype float16|bfloat16, --no-cpu, --no-pmc,
---decode-only (the decode timing alone: the command whose rocprofv3 kernel
-trace is the profile of the headline loop).
+ragged), --tokens (every sequence at that length), --splits, --value-dtype
+float16|bfloat16, --no-cpu, --no-pmc, --decode-only (the decode timing
+alone: the command whose rocprofv3 kernel trace is the profile of the
+headline loop).
 """
 
 import argparse
@@ -95,6 +96,8 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="anchor")
+    p.add_argument("--tokens", type=int, default=-1,
+                   help="every sequence's length (default: the workload's own lengths)")
     p.add_argument("--splits", type=int, default=0, help="0 = the library's choice")
     p.add_argument("--value-dtype", default="float32",
                    choices=["float32", "float16", "bfloat16"])
@@ -108,6 +111,15 @@ def parse():
                         "headline loop runs")
     p.add_argument("--pmc-child", default="", help=argparse.SUPPRESS)
     return p.parse_args()
+
+
+def workload_lens(args):
+    """Every sequence at --tokens rows, or None for the workload's own lengths."""
+    if args.tokens < 0:
+        return None
+    import numpy as np
+    from flash_decode_int4 import workloads
+    return np.full(workloads.WORKLOADS[args.workload]["batch"], args.tokens, np.int32)
 
 
 def build_sets(name, value_dtype, n_sets_hint=0, seq_lens=None):
@@ -758,7 +770,8 @@ def pmc_child(args):
     counters give the bytes/counter factors, then the fake-quantization
     workloads."""
     import torch
-    sets, _ = build_sets(args.workload, args.value_dtype, n_sets_hint=1)
+    sets, _ = build_sets(args.workload, args.value_dtype, n_sets_hint=1,
+                         seq_lens=workload_lens(args))
     r = time_decode(sets, args.splits, steps=3, warmup=1)
     time_quantizer(sets, steps=3, warmup=1)
     del sets
@@ -794,8 +807,8 @@ def pmc_traffic(args):
         d = tempfile.mkdtemp(prefix="fdi4_pmc_")
         cmd = [exe, "--pmc", counter, "-d", d, "-o", "pmc", "--output-format", "csv", "--",
                sys.executable, os.path.abspath(__file__), "--workload", args.workload,
-               "--splits", str(args.splits), "--value-dtype", args.value_dtype,
-               "--pmc-child", counter]
+               "--tokens", str(args.tokens), "--splits", str(args.splits),
+               "--value-dtype", args.value_dtype, "--pmc-child", counter]
         try:
             subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=180,
                            check=False)
@@ -878,7 +891,7 @@ def main():
               f"{ops.backend_status()}", file=sys.stderr)
         sys.exit(1)
 
-    sets, set_bytes = build_sets(args.workload, args.value_dtype)
+    sets, set_bytes = build_sets(args.workload, args.value_dtype, seq_lens=workload_lens(args))
     w0 = sets[0]["w"]
     vbytes = 4 if args.value_dtype == "float32" else 2
     qbytes = workloads.quantize_bytes(w0["seq_lens"], w0["heads"], w0["head_dim"])

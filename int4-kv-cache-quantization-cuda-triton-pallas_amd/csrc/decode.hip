@@ -8,9 +8,9 @@
 // Work decomposition (split-K flash decoding):
 //   grid (num_splits, Hq, B); a workgroup of WAVES wave64s owns one split,
 //   a contiguous range of 16-row chunks of one (sequence, q-head); every wave
-//   takes an equal contiguous sub-range (the first waves also one chunk each
-//   of the remainder, see wave_chunks), keeps its own (m, l, acc) and the
-//   waves are merged through LDS. With one split the workgroup writes the output,
+//   takes a contiguous sub-range (a quarter of the range per SIMD, split
+//   18:14 between the SIMD's older and younger wave, see wave_chunks), keeps
+//   its own (m, l, acc) and the waves are merged through LDS. With one split the workgroup writes the output,
 //   otherwise (m, l, acc[D]) goes to the workspace and merge_kernel combines
 //   the splits with a log-sum-exp weighting.
 //
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   int c = wc0;
   ChunkMeta cm, nm;
   U32x4 sz[G::SZL];
-  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, wr.chunk_at(min(ci, wc1 - 1))); };
+  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, min(ci, wc1 - 1)); };
   auto step = [&](const KVec<G::KW>* ck, const U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
     if (cm.group != cur_group) {
       float* szw = sz_s[w];
@@ -301,7 +301,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   if constexpr (STEP) {
     if (t_app >= 0) og_first = (t_app / a.step.group_rows) * a.step.group_rows / a.page_rows * cpp;
   }
-  const bool early = has_work && wr.chunk_at(c) < og_first;
+  const bool early = has_work && c < og_first;
   if (has_work) {
     cm = meta_at(c);
     nm = meta_at(c + 1);

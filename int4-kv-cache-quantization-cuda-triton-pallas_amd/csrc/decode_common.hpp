@@ -139,30 +139,38 @@ __device__ __forceinline__ int pages_of(const DecodeArgs& a, int T) {
   return T / a.page_rows + (T % a.page_rows != 0);
 }
 
-// Chunks of wave w of `waves` over the chunks [begin, end) of a split. Every
-// wave streams span / waves consecutive chunks; the span % waves chunks left
-// at the end of the split go one each to the FIRST waves, after their own
-// range. Waves 0-3 of a workgroup are the first wave on each SIMD and run
-// ahead of waves 4-7, so the remainder rides on the waves with slack: one
-// decode of B8 H32 D128 at 2049 tokens (129 chunks per sequence) takes 1.1 %
-// longer than at 2048 with the remainder on wave 0, against 2.5 % with it on
-// the last wave. The loop walks positions [c0, c1); chunk_at maps a position
-// to its chunk.
+// Chunks of wave w of `waves` (4 or 8) over the chunks [begin, end) of a
+// split, as one contiguous range per wave. Wave w runs on SIMD w % 4; every
+// SIMD takes span / 4 consecutive chunks (the first span % 4 SIMDs one more).
+// With eight waves, waves w and w + 4 share a SIMD, and the older wave w is
+// issued ahead of w + 4: with equal ranges at B8 H32 D128 T2048 (16 chunks
+// each), waves 0-3 finished their loops 6.5 us before waves 4-7 (38.6 against
+// 45.1 us), leaving one wave per SIMD, with half the loads in flight, for the
+// rest of the decode. The older wave therefore takes kFirstShare32 / 32 of
+// its SIMD's chunks (rounded to nearest) and the younger one the rest.
+#ifndef FDI4_FIRST_SHARE32
+#define FDI4_FIRST_SHARE32 18
+#endif
+constexpr int kFirstShare32 = FDI4_FIRST_SHARE32;
+
 struct WaveRange {
-  int c0, c1;      // loop positions
-  int own_end;     // positions below own_end are the wave's own chunks
-  int extra;       // the chunk at position own_end, when c1 > own_end
-  __device__ __forceinline__ int chunk_at(int pos) const { return pos < own_end ? pos : extra; }
+  int c0, c1;      // the wave's chunks [c0, c1)
 };
 
 __device__ __forceinline__ WaveRange wave_chunks(int begin, int end, int w, int waves) {
   const int span = max(end - begin, 0);
-  const int base = span / waves, rem = span - base * waves;
+  const int simds = min(waves, 4);
+  const int s = w % simds;
+  const int base = span / simds, rem = span - base * simds;
   WaveRange r;
-  r.c0 = begin + w * base;
-  r.own_end = r.c0 + base;
-  r.extra = begin + waves * base + w;
-  r.c1 = r.own_end + (w < rem ? 1 : 0);
+  r.c0 = begin + s * base + min(s, rem);
+  const int n = base + (s < rem ? 1 : 0);
+  r.c1 = r.c0 + n;
+  if (waves > simds) {
+    const int first = (n * kFirstShare32 + 16) / 32;
+    if (w < simds) r.c1 = r.c0 + first;
+    else r.c0 += first;
+  }
   return r;
 }
 

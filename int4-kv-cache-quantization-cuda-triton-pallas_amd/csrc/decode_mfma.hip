@@ -221,7 +221,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(DecodeArgs a) {
   int c = wc0;
   ChunkMeta cm, nm;
   U32x4 sz[G::SZL];
-  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, wr.chunk_at(min(ci, wc1 - 1))); };
+  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, min(ci, wc1 - 1)); };
   auto step = [&](const KVec<G::KW>* ck, const U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
     if (cm.group != cur_group) {
       float* szw = sz_s[w];
