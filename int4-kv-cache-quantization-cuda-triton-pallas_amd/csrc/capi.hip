@@ -646,8 +646,10 @@ int fdi4_decode_step(const void* query, int query_dtype, int batch, int num_q_he
                         cache, 0, &a);
   if (rc != hipSuccess) return rc;
   if (!out || !valid_elem_dtype(out_dtype)) return hipErrorInvalidValue;
-  // One workgroup per (sequence, kv-head): the append fuses into the decode.
-  const bool fused = a.num_splits == 1 && !a.mfma && a.heads_per_wg == 1 && a.hq_per_kv == 1;
+  // One workgroup per (sequence, kv-head): the append fuses into the decode
+  // (whose reads of a group's staging rows take 32-bit byte offsets).
+  const bool fused = a.num_splits == 1 && !a.mfma && a.heads_per_wg == 1 && a.hq_per_kv == 1 &&
+                     (int64_t)group_rows * st_row_stride * 4 <= INT32_MAX;
   if (!fused) {
     // Two launches: the append writes the advanced lengths to lens_next, the
     // decode attends over them and copies them back to the cache's lengths.

@@ -60,14 +60,15 @@ struct Geo {
 // The fused serving step's append (STEP instantiations): this workgroup
 // writes token t of its (sequence, kv-head) and re-quantizes the open group
 // (step_requant).
-template <int D, int NT, int VEB>
-__device__ __forceinline__ void step_append(const DecodeArgs& a, int b, int hk, int t) {
-  step_requant<D, NT, VEB>(a.step, const_cast<uint8_t*>(a.k_pages), a.k_page, a.k_head, a.k_row,
+template <int D, int NT, int VEB, typename Issue>
+__device__ __forceinline__ void step_append(Issue&& issue, const DecodeArgs& a, int b, int hk,
+                                            int t, uint16_t* k_open, float* sz_open) {
+  step_requant<D, NT, VEB>(issue, a.step, const_cast<uint8_t*>(a.k_pages), a.k_page, a.k_head, a.k_row,
                            reinterpret_cast<uint8_t*>(const_cast<void*>(a.v_pages)),
                            a.v_page * VEB, a.v_head * VEB, a.v_row * VEB,
                            const_cast<float*>(a.k_scale), const_cast<float*>(a.k_zp), a.s_b,
                            a.s_h, a.s_g, a.page_table, a.pt_b, a.page_rows, a.num_pages, b, hk,
-                           t);
+                           t, k_open, sz_open);
 }
 
 // The fused serving step's length advance: every workgroup of sequence b
@@ -108,6 +109,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   __shared__ float acc_s[WAVES][D];
   __shared__ double m_s[WAVES];
   __shared__ float l_s[WAVES];
+  // With STEP: the open group's packed rows and scale/zero-point, as the
+  // re-quantization left them (step_requant).
+  __shared__ uint16_t k_open[STEP ? kStepMaxGroup * D / 4 : 1];
+  __shared__ float sz_open[STEP ? 2 * D : 1];
 
   const int cpp = (a.page_rows + 15) >> 4;
   // With STEP, token t_app = seq_lens[b] is appended (none when the sequence
@@ -121,6 +126,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   } else {
     T = seq_len_of(a, b);
   }
+  // With a token to append, the open group's keys and scales come from
+  // k_open / sz_open and row t_app's values from v_new while the cache's
+  // copies are being written.
+  const bool append = STEP && t_app >= 0;
+  const int open_g = append ? t_app / a.step.group_rows : -1;
   const int n_chunks = pages_of(a, T) * cpp;
   const int c_begin = split * a.chunks_per_split;
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
@@ -146,6 +156,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   const uint8_t* vbase_h = reinterpret_cast<const uint8_t*>(a.v_pages) +
                            (int64_t)hk * a.v_head * G::VEB;
   const unsigned k_lane = kq * G::KBL, v_lane = vcol * 16;
+  const uint8_t* vnew = nullptr;
+  if constexpr (STEP) vnew = a.step.v_new + (int64_t)b * a.step.vn_b + (int64_t)hk * a.step.vn_h;
   const unsigned krow_b = (unsigned)a.k_row, vrow_b = (unsigned)(a.v_row * G::VEB);
 
   // Scale/zero-point block of one group: items 0..D/4-1 are scale[4e..4e+3],
@@ -171,7 +183,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < G::VLD; ++i) {
       const int r = max(min(i * G::RPL + vrow, m.nval - 1), 0);
-      vr[i] = ld16_stream(vb + (v_lane + (unsigned)r * vrow_b));
+      const uint8_t* src = vb + (v_lane + (unsigned)r * vrow_b);
+      // With STEP, row t_app's values come from v_new (the cache's row is
+      // being written meanwhile); with one row per sweep the choice is
+      // wave-uniform and the load keeps its scalar base.
+      if constexpr (STEP && G::RPL == 1) {
+        const uint8_t* base = (m.tok0 + r == t_app) ? vnew : vb + (unsigned)r * vrow_b;
+        src = base + v_lane;
+      } else if constexpr (STEP) {
+        if (m.tok0 + r == t_app) src = vnew + v_lane;
+      }
+      vr[i] = ld16_stream(src);
     }
   };
 
@@ -184,16 +206,19 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   // on the prefetch. An empty chunk (page_lens 0) is loaded from row 0 of its
   // page and skipped.
   int c = wc0;
-  ChunkMeta cm, nm;
+  ChunkMeta cm{}, nm{};
   U32x4 sz[G::SZL];
   auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, min(ci, wc1 - 1)); };
-  auto step = [&](const KVec<G::KW>* ck, const U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
+  auto step = [&](KVec<G::KW>* ck, const U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
     if (cm.group != cur_group) {
-      float* szw = sz_s[w];
+      const bool open = STEP && cm.group == open_g;
+      float* szw = open ? sz_open : sz_s[w];
+      if (!open) {
 #pragma unroll
-      for (int i = 0; i < G::SZL; ++i) {
-        const int e = i * 64 + lane;
-        if (e < G::SZI) *reinterpret_cast<U32x4*>(szw + 4 * e) = sz[i];
+        for (int i = 0; i < G::SZL; ++i) {
+          const int e = i * 64 + lane;
+          if (e < G::SZI) *reinterpret_cast<U32x4*>(szw + 4 * e) = sz[i];
+        }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -224,6 +249,19 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     const ChunkMeta nnm = meta_at(c + 2);
     if (cm.nval > 0) {
 
+    // Keys of the open group (STEP) from k_open: the cache's copy is being
+    // written meanwhile, and the loads of it into ck are not used.
+    if constexpr (STEP) {
+      if (cm.group == open_g) {
+#pragma unroll
+        for (int i = 0; i < G::KLD; ++i) {
+          const int t = max(min(i * G::TPW + ktok, cm.nval - 1), 0);
+          const int row = cm.tok0 + t - open_g * a.step.group_rows;
+          ck[i] = *reinterpret_cast<const KVec<G::KW>*>(
+              reinterpret_cast<const uint8_t*>(k_open) + row * (D / 2) + k_lane);
+        }
+      }
+    }
     double lg[G::KLD];
 #pragma unroll
     for (int i = 0; i < G::KLD; ++i) {
@@ -294,28 +332,26 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   const bool has_work = c < wc1;
   KVec<G::KW> ka[G::KLD], kb[G::KLD];
   U32x4 va[G::VLD], vb[G::VLD];
-  // With STEP the first chunk's loads go out before the append when the chunk
-  // lies before the open group (first chunk og_first), so its latency
-  // overlaps the re-quantization; a chunk of the open group is loaded after.
-  int og_first = INT_MAX;
-  if constexpr (STEP) {
-    if (t_app >= 0) og_first = (t_app / a.step.group_rows) * a.step.group_rows / a.page_rows * cpp;
-  }
-  const bool early = has_work && c < og_first;
-  if (has_work) {
-    cm = meta_at(c);
-    nm = meta_at(c + 1);
-  }
-  if (early) {
-    load_sz(cm, sz);
-    load_chunk(cm, ka, va);
-  }
-  if constexpr (STEP) {
-    if (t_app >= 0) step_append<D, NT, G::VEB>(a, b, hk, t_app);
-  }
-  if (has_work && !early) {
-    load_sz(cm, sz);
-    load_chunk(cm, ka, va);
+  // With STEP the first chunk's loads go out right after the re-quantization's
+  // first rows, so their latency overlaps the re-quantization (a chunk of the
+  // open group takes its keys and scales from LDS, so loading the cache's
+  // copy early is fine).
+  // Inside the re-quantization the loads are unconditional (a wave without
+  // chunks loads chunk 0, which exists there, and ignores it): loads under a
+  // branch would make the re-quantization's waits drain them.
+  auto first_loads = [&](bool always) {
+    if (has_work) nm = meta_at(c + 1);
+    if (has_work || always) {
+      cm = chunk_meta(a, b, T, cpp, has_work ? min(c, wc1 - 1) : 0);
+      load_sz(cm, sz);
+      load_chunk(cm, ka, va);
+    }
+  };
+  if (append) {
+    if constexpr (STEP)
+      step_append<D, NT, G::VEB>([&] { first_loads(true); }, a, b, hk, t_app, k_open, sz_open);
+  } else {
+    first_loads(false);
   }
   if (tid < D) q_s[tid] = qv;
   __syncthreads();

@@ -93,6 +93,7 @@ struct ChunkMeta {
   int r0;
   int nval;
   int group;
+  int tok0;        // logical row of the chunk's first row
 };
 
 __device__ __forceinline__ ChunkMeta chunk_meta(const DecodeArgs& a, int b, int T, int cpp,
@@ -111,6 +112,7 @@ __device__ __forceinline__ ChunkMeta chunk_meta(const DecodeArgs& a, int b, int 
   const int pg = a.page_table ? ld_ro(a.page_table, (int64_t)b * a.pt_b + lp) : lp;
   m.phys = (int64_t)min(max(pg, 0), a.num_pages - 1);
   m.group = lp / a.pages_per_group;
+  m.tok0 = lp * a.page_rows + m.r0;
   return m;
 }
 
