@@ -62,13 +62,14 @@ struct Geo {
 // (step_requant).
 template <int D, int NT, int VEB, typename Issue>
 __device__ __forceinline__ void step_append(Issue&& issue, const DecodeArgs& a, int b, int hk,
-                                            int t, uint16_t* k_open, float* sz_open) {
+                                            int t, uint16_t* k_open, float* sz_open,
+                                            U32x4* v_open) {
   step_requant<D, NT, VEB>(issue, a.step, const_cast<uint8_t*>(a.k_pages), a.k_page, a.k_head, a.k_row,
                            reinterpret_cast<uint8_t*>(const_cast<void*>(a.v_pages)),
                            a.v_page * VEB, a.v_head * VEB, a.v_row * VEB,
                            const_cast<float*>(a.k_scale), const_cast<float*>(a.k_zp), a.s_b,
                            a.s_h, a.s_g, a.page_table, a.pt_b, a.page_rows, a.num_pages, b, hk,
-                           t, k_open, sz_open);
+                           t, k_open, sz_open, v_open);
 }
 
 // The fused serving step's length advance: every workgroup of sequence b
@@ -113,6 +114,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   // re-quantization left them (step_requant).
   __shared__ uint16_t k_open[STEP ? kStepMaxGroup * D / 4 : 1];
   __shared__ float sz_open[STEP ? 2 * D : 1];
+  __shared__ U32x4 v_open[STEP ? D * G::VEB / 16 : 1];
 
   const int cpp = (a.page_rows + 15) >> 4;
   // With STEP, token t_app = seq_lens[b] is appended (none when the sequence
@@ -127,7 +129,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     T = seq_len_of(a, b);
   }
   // With a token to append, the open group's keys and scales come from
-  // k_open / sz_open and row t_app's values from v_new while the cache's
+  // k_open / sz_open and row t_app's values from v_open while the cache's
   // copies are being written.
   const bool append = STEP && t_app >= 0;
   const int open_g = append ? t_app / a.step.group_rows : -1;
@@ -156,8 +158,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   const uint8_t* vbase_h = reinterpret_cast<const uint8_t*>(a.v_pages) +
                            (int64_t)hk * a.v_head * G::VEB;
   const unsigned k_lane = kq * G::KBL, v_lane = vcol * 16;
-  const uint8_t* vnew = nullptr;
-  if constexpr (STEP) vnew = a.step.v_new + (int64_t)b * a.step.vn_b + (int64_t)hk * a.step.vn_h;
   const unsigned krow_b = (unsigned)a.k_row, vrow_b = (unsigned)(a.v_row * G::VEB);
 
   // Scale/zero-point block of one group: items 0..D/4-1 are scale[4e..4e+3],
@@ -183,17 +183,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < G::VLD; ++i) {
       const int r = max(min(i * G::RPL + vrow, m.nval - 1), 0);
-      const uint8_t* src = vb + (v_lane + (unsigned)r * vrow_b);
-      // With STEP, row t_app's values come from v_new (the cache's row is
-      // being written meanwhile); with one row per sweep the choice is
-      // wave-uniform and the load keeps its scalar base.
-      if constexpr (STEP && G::RPL == 1) {
-        const uint8_t* base = (m.tok0 + r == t_app) ? vnew : vb + (unsigned)r * vrow_b;
-        src = base + v_lane;
-      } else if constexpr (STEP) {
-        if (m.tok0 + r == t_app) src = vnew + v_lane;
-      }
-      vr[i] = ld16_stream(src);
+      vr[i] = ld16_stream(vb + (v_lane + (unsigned)r * vrow_b));
     }
   };
 
@@ -209,7 +199,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   ChunkMeta cm{}, nm{};
   U32x4 sz[G::SZL];
   auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, min(ci, wc1 - 1)); };
-  auto step = [&](KVec<G::KW>* ck, const U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
+  auto step = [&](KVec<G::KW>* ck, U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
     if (cm.group != cur_group) {
       const bool open = STEP && cm.group == open_g;
       float* szw = open ? sz_open : sz_s[w];
@@ -303,6 +293,19 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    // Row t_app's values (STEP) from v_open: the cache's row is being written
+    // meanwhile, and the loads of it into cv (also those of lanes past the
+    // valid rows, which load the last valid row) are not used.
+    if constexpr (STEP) {
+      if ((unsigned)(t_app - cm.tok0) < (unsigned)cm.nval) {
+        const U32x4 vo = v_open[v_lane / 16];
+#pragma unroll
+        for (int i = 0; i < G::VLD; ++i) {
+          const int r = max(min(i * G::RPL + vrow, cm.nval - 1), 0);
+          if (cm.tok0 + r == t_app) cv[i] = vo;
+        }
+      }
+    }
 #pragma unroll
     for (int k = 0; k < G::VCL; ++k) acc[k] *= corr;
 #pragma unroll
@@ -349,7 +352,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   };
   if (append) {
     if constexpr (STEP)
-      step_append<D, NT, G::VEB>([&] { first_loads(true); }, a, b, hk, t_app, k_open, sz_open);
+      step_append<D, NT, G::VEB>([&] { first_loads(true); }, a, b, hk, t_app, k_open, sz_open,
+                                 v_open);
   } else {
     first_loads(false);
   }

@@ -54,12 +54,12 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 // (quant_bin_rc, scale_zp), so the stored bytes equal the append kernel's.
 // k_pages/v_pages and the scales are the cache's (byte and element strides
 // as in DecodeArgs; the group's rows lie in mapped pages). The group's packed
-// rows (row r at byte r * D / 2) and its scale and zero-point (scale of
-// channel d at d, zero-point at D + d) are also left in the workgroup's LDS,
-// k_open and sz_open, visible to every wave on return. The stores to the
-// cache are issued, not awaited: until the kernel ends, the workgroup reads
-// the open group from k_open / sz_open and the new value row from v_new,
-// never from the cache.
+// rows (row r at byte r * D / 2), its scale and zero-point (scale of channel
+// d at d, zero-point at D + d) and the new value row are also left in the
+// workgroup's LDS, k_open, sz_open and v_open, visible to every wave on
+// return. The stores to the cache are issued, not awaited: until the kernel
+// ends, the workgroup reads the open group's keys and scales and the new
+// value row from LDS, never from the cache.
 //
 // issue() is called once, right after this function's own loads of the
 // first batch of rows, the new rows and the group's page-table entries: the
@@ -77,7 +77,7 @@ __device__ __forceinline__ void step_requant(Issue&& issue, const StepAppend& s,
                                              int64_t s_b, int64_t s_h, int64_t s_g,
                                              const int32_t* page_table, int64_t pt_b,
                                              int page_rows, int num_pages, int b, int h, int t,
-                                             uint16_t* k_open, float* sz_open) {
+                                             uint16_t* k_open, float* sz_open, U32x4* v_open) {
   constexpr int VPR = D / 4;          // threads per staged row (16 bytes each)
   constexpr int RPI = NT / VPR;       // rows per sweep of the workgroup
   constexpr int NI = kStepMaxGroup / RPI;   // rows per thread, at most
@@ -178,6 +178,7 @@ __device__ __forceinline__ void step_requant(Issue&& issue, const StepAppend& s,
   st16(v_pages + (int64_t)pt_grp[rnew / page_rows] * vp_page + (int64_t)h * vp_head +
            (int64_t)(t % page_rows) * vp_row + 16 * vpiece,
        vcopy);
+  if (tid < VPC) v_open[tid] = vcopy;
 #pragma unroll
   for (int w = 0; w < NWAVE; ++w) {
     const float4 pm = q_mn[w][cq], px = q_mx[w][cq];
