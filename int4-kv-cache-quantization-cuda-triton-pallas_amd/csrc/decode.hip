@@ -57,19 +57,19 @@ struct Geo {
   static_assert(RPL >= 1 && 16 % RPL == 0 && 16 % TPW == 0, "geometry");
 };
 
-// The fused serving step's append (STEP instantiations): this workgroup
-// writes token t of its (sequence, kv-head) and re-quantizes the open group
-// (step_requant).
-template <int D, int NT, int VEB, typename Issue>
-__device__ __forceinline__ void step_append(Issue&& issue, const DecodeArgs& a, int b, int hk,
-                                            int t, uint16_t* k_open, float* sz_open,
-                                            U32x4* v_open) {
-  step_requant<D, NT, VEB>(issue, a.step, const_cast<uint8_t*>(a.k_pages), a.k_page, a.k_head, a.k_row,
-                           reinterpret_cast<uint8_t*>(const_cast<void*>(a.v_pages)),
-                           a.v_page * VEB, a.v_head * VEB, a.v_row * VEB,
-                           const_cast<float*>(a.k_scale), const_cast<float*>(a.k_zp), a.s_b,
-                           a.s_h, a.s_g, a.page_table, a.pt_b, a.page_rows, a.num_pages, b, hk,
-                           t, k_open, sz_open, v_open);
+// The fused serving step's append (STEP instantiations): the calling wave
+// re-quantizes channel quarter `slice` of the open group of token t of its
+// (sequence, kv-head) (step_requant_slice); four waves make the whole append.
+template <int D, int VEB>
+__device__ __forceinline__ void step_append(const DecodeArgs& a, int b, int hk, int t, int slice,
+                                            int lane, uint16_t* k_open, float* sz_open,
+                                            U32x4* v_open, int* pt_w) {
+  step_requant_slice<D, VEB>(a.step, const_cast<uint8_t*>(a.k_pages), a.k_page, a.k_head,
+                             a.k_row, reinterpret_cast<uint8_t*>(const_cast<void*>(a.v_pages)),
+                             a.v_page * VEB, a.v_head * VEB, a.v_row * VEB,
+                             const_cast<float*>(a.k_scale), const_cast<float*>(a.k_zp), a.s_b,
+                             a.s_h, a.s_g, a.page_table, a.pt_b, a.page_rows, a.num_pages, b, hk,
+                             t, slice, lane, k_open, sz_open, v_open, pt_w);
 }
 
 // The fused serving step's length advance: every workgroup of sequence b
@@ -111,10 +111,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   __shared__ double m_s[WAVES];
   __shared__ float l_s[WAVES];
   // With STEP: the open group's packed rows and scale/zero-point, as the
-  // re-quantization left them (step_requant).
+  // re-quantization left them (step_requant_slice).
   __shared__ uint16_t k_open[STEP ? kStepMaxGroup * D / 4 : 1];
   __shared__ float sz_open[STEP ? 2 * D : 1];
   __shared__ U32x4 v_open[STEP ? D * G::VEB / 16 : 1];
+  // With STEP: each re-quantizing wave's copy of the group's page-table
+  // entries, and the count of waves whose quarter of the append is in LDS.
+  __shared__ int pt_w[STEP ? 4 : 1][STEP ? kStepMaxGroup : 1];
+  __shared__ int open_done;
 
   const int cpp = (a.page_rows + 15) >> 4;
   // With STEP, token t_app = seq_lens[b] is appended (none when the sequence
@@ -202,6 +206,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   auto step = [&](KVec<G::KW>* ck, U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
     if (cm.group != cur_group) {
       const bool open = STEP && cm.group == open_g;
+      // The open group's keys, scales and new value row are read from LDS
+      // once all four quarters of the append are there (each re-quantizing
+      // wave counts itself in after its last LDS write; none of them waits
+      // on another wave first, so the count always reaches four).
+      if (open) {
+        while (__hip_atomic_load(&open_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < 4)
+          __builtin_amdgcn_s_sleep(2);
+      }
       float* szw = open ? sz_open : sz_s[w];
       if (!open) {
 #pragma unroll
@@ -335,30 +347,36 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   const bool has_work = c < wc1;
   KVec<G::KW> ka[G::KLD], kb[G::KLD];
   U32x4 va[G::VLD], vb[G::VLD];
-  // With STEP the first chunk's loads go out right after the re-quantization's
-  // first rows, so their latency overlaps the re-quantization (a chunk of the
-  // open group takes its keys and scales from LDS, so loading the cache's
-  // copy early is fine).
-  // Inside the re-quantization the loads are unconditional (a wave without
-  // chunks loads chunk 0, which exists there, and ignores it): loads under a
-  // branch would make the re-quantization's waits drain them.
-  auto first_loads = [&](bool always) {
-    if (has_work) nm = meta_at(c + 1);
-    if (has_work || always) {
-      cm = chunk_meta(a, b, T, cpp, has_work ? min(c, wc1 - 1) : 0);
-      load_sz(cm, sz);
-      load_chunk(cm, ka, va);
-    }
+  // A re-quantizing wave (STEP) loads its first chunk after its quarter of
+  // the append where the chunk's registers would not fit beside the rows
+  // (head_dim 256, float32 values).
+  constexpr bool kLateFirst = STEP && D == 256 && VDT == kVF32;
+  const bool rq_wave = STEP && append && w >= WAVES - 4;
+  auto first_loads = [&]() {
+    cm = meta_at(c);
+    nm = meta_at(c + 1);
+    load_sz(cm, sz);
+    load_chunk(cm, ka, va);
   };
-  if (append) {
-    if constexpr (STEP)
-      step_append<D, NT, G::VEB>([&] { first_loads(true); }, a, b, hk, t_app, k_open, sz_open,
-                                 v_open);
-  } else {
-    first_loads(false);
+  if (has_work && !(kLateFirst && rq_wave)) first_loads();
+  if constexpr (STEP) {
+    if (tid == 0) open_done = 0;
   }
   if (tid < D) q_s[tid] = qv;
   __syncthreads();
+  // With a token to append, the last four waves (with eight, the second wave
+  // of each SIMD, whose delay the first waves' streaming absorbs) each
+  // re-quantize a quarter of the open group's channels, then decode.
+  if constexpr (STEP) {
+    if (rq_wave) {
+      const int slice = w - (WAVES - 4);
+      step_append<D, G::VEB>(a, b, hk, t_app, slice, lane, k_open, sz_open, v_open, pt_w[slice]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0)
+        __hip_atomic_fetch_add(&open_done, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (kLateFirst && has_work) first_loads();
+    }
+  }
   if (has_work) {
     while (true) {
       if (step(ka, va, kb, vb)) break;

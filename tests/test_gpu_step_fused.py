@@ -1,7 +1,8 @@
 """The one-launch serving step (fdi4_decode_step with one decode workgroup per
 (sequence, kv-head)): every workgroup appends its token, re-quantizes the
-open scale group, decodes over the advanced length, and the last workgroup
-of a sequence advances its length. Checked bit for bit against the
+open scale group (four waves, a quarter of the channels each, with no
+workgroup barrier, while the other waves decode), decodes over the advanced
+length, and the last workgroup of a sequence advances its length. Checked bit for bit against the
 three-launch form (append kernel, a length increment, decode) on twin
 caches, over steps that cross page and group boundaries, for every value
 type, head_dim 64/128/256, page sizes 16/32 and groups 64/128/256; replayed
