@@ -100,29 +100,49 @@ __device__ __forceinline__ void step_requant_slice(const StepAppend& s, uint8_t*
   const __amdgpu_buffer_rsrc_t srows = __builtin_amdgcn_make_buffer_rsrc(
       stage, (short)0, (int)((int64_t)rnew * s.st_r * 4), kBufferRsrcWord3);
   const float4 kcopy = *reinterpret_cast<const float4*>(knew + ch);
-  auto row = [&](int i) -> float4 {
-    const int r = rsub + i * RPL;
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-        srows, (int)((int64_t)r * s.st_r * 4) + 4 * ch, 0, 0);
-    const float4 f = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]),
-                                 __uint_as_float(v[2]), __uint_as_float(v[3]));
-    return r < rnew ? f : kcopy;
-  };
+  // Slot i of batch bt holds row rsub + (bt * NB + i) * RPL as loaded (zeros
+  // at and past row rnew); val() gives the row's keys, the new row's for rows
+  // rnew and beyond (which leaves the min/max unchanged).
   float4 x[NB];
   auto load_batch = [&](int bt) {
 #pragma unroll
-    for (int i = 0; i < NB; ++i) x[i] = row(bt * NB + i);
+    for (int i = 0; i < NB; ++i) {
+      const int r = rsub + (bt * NB + i) * RPL;
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+          srows, (int)((int64_t)r * s.st_r * 4) + 4 * ch, 0, 0);
+      x[i] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                         __uint_as_float(v[3]));
+    }
   };
-  // The group's page-table entries into pt_w, and this slice's piece of the
-  // new value row.
-  for (int j = lane; j < npg; j += 64) {
-    const int pg = page_table ? page_table[(int64_t)b * pt_b + r0 / page_rows + j]
-                              : r0 / page_rows + j;
-    pt_w[j] = min(max(pg, 0), num_pages - 1);
-  }
+  auto val = [&](int bt, int i) -> float4 {
+    return rsub + (bt * NB + i) * RPL < rnew ? x[i] : kcopy;
+  };
+  auto minmax = [&](int bt, float* mn, float* mx) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const float4 y = val(bt, i);
+      mn[0] = fminf(mn[0], y.x); mx[0] = fmaxf(mx[0], y.x);
+      mn[1] = fminf(mn[1], y.y); mx[1] = fmaxf(mx[1], y.y);
+      mn[2] = fminf(mn[2], y.z); mx[2] = fmaxf(mx[2], y.z);
+      mn[3] = fminf(mn[3], y.w); mx[3] = fmaxf(mx[3], y.w);
+    }
+  };
+  // One memory round: the first batch of rows, this slice's piece of the
+  // new value row and the group's page-table entries (lane j: page j) are
+  // all in flight before anything waits for them.
+  load_batch(0);
   const uint8_t* vsrc = s.v_new + (int64_t)b * s.vn_b + (int64_t)h * s.vn_h;
   const int vpc = slice * VPS + min(lane, VPS - 1);
   const U32x4 vcopy = ld16(vsrc + 16 * vpc);
+  const int64_t pt0 = (int64_t)b * pt_b + r0 / page_rows;
+  int pg = r0 / page_rows + lane;
+  if (page_table && lane < npg) pg = page_table[pt0 + lane];
+  if (lane < npg) pt_w[lane] = min(max(pg, 0), num_pages - 1);
+  // Groups of more than 64 pages (pages of fewer than four rows).
+  for (int j = lane + 64; j < npg; j += 64) {
+    const int pj = page_table ? page_table[pt0 + j] : r0 / page_rows + j;
+    pt_w[j] = min(max(pj, 0), num_pages - 1);
+  }
 
   float mn[4], mx[4];
 #pragma unroll
@@ -130,17 +150,13 @@ __device__ __forceinline__ void step_requant_slice(const StepAppend& s, uint8_t*
     mn[k] = INFINITY;
     mx[k] = -INFINITY;
   }
+  minmax(0, mn, mx);
+  const int nbu = rnew / (NB * RPL) + 1;   // batches holding rows 0..rnew
+  if constexpr (NBATCH > 1) {
 #pragma unroll 1
-  for (int bt = 0; bt < NBATCH; ++bt) {
-    if (bt * NB * RPL <= rnew) {
+    for (int bt = 1; bt < nbu; ++bt) {
       load_batch(bt);
-#pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        mn[0] = fminf(mn[0], x[i].x); mx[0] = fmaxf(mx[0], x[i].x);
-        mn[1] = fminf(mn[1], x[i].y); mx[1] = fmaxf(mx[1], x[i].y);
-        mn[2] = fminf(mn[2], x[i].z); mx[2] = fmaxf(mx[2], x[i].z);
-        mn[3] = fminf(mn[3], x[i].w); mx[3] = fmaxf(mx[3], x[i].w);
-      }
+      minmax(bt, mn, mx);
     }
   }
 #pragma unroll
@@ -174,27 +190,28 @@ __device__ __forceinline__ void step_requant_slice(const StepAppend& s, uint8_t*
   }
 
   // Bins of the valid rows: this lane's 4 channels of each of its rows, two
-  // bytes of the packed row, into k_open and the row's page.
+  // bytes of the packed row, into k_open and the row's page. The last batch
+  // is still in registers; earlier ones (groups of more rows than one batch)
+  // are loaded again.
 #pragma unroll 1
-  for (int bt = 0; bt < NBATCH; ++bt) {
-    if (bt * NB * RPL <= rnew) {
-      if (NBATCH > 1) load_batch(bt);
+  for (int bt = nbu - 1; bt >= 0; --bt) {
+    if (NBATCH > 1 && bt != nbu - 1) load_batch(bt);
 #pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        const int r = rsub + (bt * NB + i) * RPL;
-        if (r <= rnew) {
-          const float n0 = quant_bin_rc(x[i].x, mn[0], sc[0], rc[0]);
-          const float n1 = quant_bin_rc(x[i].y, mn[1], sc[1], rc[1]);
-          const float n2 = quant_bin_rc(x[i].z, mn[2], sc[2], rc[2]);
-          const float n3 = quant_bin_rc(x[i].w, mn[3], sc[3], rc[3]);
-          const uint16_t pk = (uint16_t)(unsigned)__builtin_fmaf(
-              n3, 4096.0f, __builtin_fmaf(n2, 256.0f, __builtin_fmaf(n1, 16.0f, n0)));
-          k_open[r * (D / 4) + ch / 4] = pk;
-          const int tok = r0 + r;
-          *reinterpret_cast<uint16_t*>(k_pages + (int64_t)pt_w[r / page_rows] * kp_page +
-                                       (int64_t)h * kp_head +
-                                       (int64_t)(tok % page_rows) * kp_row + ch / 2) = pk;
-        }
+    for (int i = 0; i < NB; ++i) {
+      const int r = rsub + (bt * NB + i) * RPL;
+      if (r <= rnew) {
+        const float4 y = val(bt, i);
+        const float n0 = quant_bin_rc(y.x, mn[0], sc[0], rc[0]);
+        const float n1 = quant_bin_rc(y.y, mn[1], sc[1], rc[1]);
+        const float n2 = quant_bin_rc(y.z, mn[2], sc[2], rc[2]);
+        const float n3 = quant_bin_rc(y.w, mn[3], sc[3], rc[3]);
+        const uint16_t pk = (uint16_t)(unsigned)__builtin_fmaf(
+            n3, 4096.0f, __builtin_fmaf(n2, 256.0f, __builtin_fmaf(n1, 16.0f, n0)));
+        k_open[r * (D / 4) + ch / 4] = pk;
+        const int tok = r0 + r;
+        *reinterpret_cast<uint16_t*>(k_pages + (int64_t)pt_w[r / page_rows] * kp_page +
+                                     (int64_t)h * kp_head +
+                                     (int64_t)(tok % page_rows) * kp_row + ch / 2) = pk;
       }
     }
   }
