@@ -566,29 +566,41 @@ def time_other_paths(args):
 
 def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8):
     """The serving loop's step on the sequence cache (fp32 values, B sequences
-    of H heads from T tokens): append one token per (sequence, kv-head),
+    of H heads around T tokens): append one token per (sequence, kv-head),
     decode over the advanced lengths, advance them -- one launch when each
-    (sequence, kv-head) is one decode workgroup (fdi4_decode_step). Timed in
-    rounds, each of `graph_steps` steps issued eagerly from Python, then the
-    same number replayed from a graph holding one step, then one replay of a
-    graph holding `graph_steps` steps (the graph launch's own cost spread over
-    them); every step adds a token, and the interleaving gives the three
-    forms the same lengths. Medians over the rounds, per step."""
+    (sequence, kv-head) is one decode workgroup (fdi4_decode_step). Every
+    timed segment is one scale group of steps (group_rows = 128) from the same
+    state, T - 64 tokens, restored before it (the device lengths and the open
+    group's staging rows), so a segment re-quantizes every row count of a
+    group once and its mean length is T - 0.5: the steps issued eagerly from
+    Python, one-step graph replays, and replays of a graph of `graph_steps`
+    steps (the graph launch's own cost spread over them). Medians over the
+    rounds, per step; `decode_us` is the plain decode of the same cache at T
+    tokens."""
     import torch
     from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
-    rounds = max(4, args.steps // (3 * graph_steps))
-    n = args.warmup + 3 * rounds * graph_steps + 4 * graph_steps
-    cache = INT4PagedSequenceCache(num_pages=B * ((T + n) // 16 + 2), num_kv_heads=H, head_dim=D,
-                                   max_seqs=B, max_seq_len=T + n)
+    G = 128
+    T0 = T - G // 2
+    rounds = 4
+    cache = INT4PagedSequenceCache(num_pages=B * ((T0 + G) // 16 + 2), num_kv_heads=H,
+                                   head_dim=D, max_seqs=B, max_seq_len=T0 + G, group_rows=G)
     g = torch.Generator(device="cuda")
     g.manual_seed(3)
-    k = torch.randn(B, H, T, D, device="cuda", generator=g)
-    cache.prefill(k, torch.randn_like(k), [T] * B)
+    k = torch.randn(B, H, T0, D, device="cuda", generator=g)
+    cache.prefill(k, torch.randn_like(k), [T0] * B)
     del k
-    cache.reserve(B, n)
+    cache.reserve(B, G)
+    stage0 = cache.k_stage.clone()
     kn = torch.randn(B, H, D, device="cuda", generator=g)
     vn = torch.randn(B, H, D, device="cuda", generator=g)
     q = torch.randn(B, H, D, device="cuda", generator=g)
+
+    def restore(length=T0):
+        torch.cuda.synchronize()
+        cache.seq_lens[:B].fill_(length)
+        cache.k_stage.copy_(stage0)
+        torch.cuda.synchronize()
+        cache.sync_lengths()
 
     def timed(fn, reps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -600,9 +612,9 @@ def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3
 
-    for _ in range(args.warmup):
+    for _ in range(min(args.warmup, G)):
         cache.step(kn, vn, q)
-    torch.cuda.synchronize()
+    restore()
     graph_1 = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph_1):
         out_1 = cache.step(kn, vn, q)
@@ -612,16 +624,24 @@ def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8):
             out_k = cache.step(kn, vn, q)
     eager, rep_1, rep_k = [], [], []
     for _ in range(rounds):
-        eager.append(timed(lambda: cache.step(kn, vn, q), graph_steps) / graph_steps)
-        rep_1.append(timed(graph_1.replay, graph_steps) / graph_steps)
-        rep_k.append(timed(graph_k.replay, 1) / graph_steps)
+        restore()
+        eager.append(timed(lambda: cache.step(kn, vn, q), G) / G)
+        restore()
+        rep_1.append(timed(graph_1.replay, G) / G)
+        restore()
+        rep_k.append(timed(graph_k.replay, G // graph_steps) / G)
     ok = bool(torch.isfinite(out_1).all()) and bool(torch.isfinite(out_k).all())
     cache.sync_lengths()
-    res = {"workload": f"B{B} H{H} D{D} from {T} tokens, fp32 values: append + decode + "
-                       "length advance per step",
+    end_len = int(cache.lengths()[0])
+    restore(T)
+    dec = median([timed(lambda: cache.decode(q), 20) / 20 for _ in range(rounds)])
+    res = {"workload": f"B{B} H{H} D{D}, fp32 values: append + decode + length advance per "
+                       f"step, steps from {T0} to {T0 + G} tokens (one {G}-token scale group, "
+                       f"mean {T - 0.5})",
            "eager_us": round(median(eager), 3), "graph_replay_us": round(median(rep_1), 3),
            f"graph_{graph_steps}_steps_replay_us_per_step": round(median(rep_k), 3),
-           "rounds": rounds, "finite": ok, "final_length": int(cache.lengths()[0])}
+           "decode_us": round(dec, 3), "rounds": rounds, "finite": ok,
+           "final_length": end_len}
     del cache, graph_1, graph_k
     torch.cuda.empty_cache()
     return res

@@ -7,10 +7,12 @@
 //
 // Work decomposition (split-K flash decoding):
 //   grid (num_splits, Hq, B); a workgroup of WAVES wave64s owns one split,
-//   a contiguous range of 16-row chunks of one (sequence, q-head); every wave
-//   takes a contiguous sub-range (a quarter of the range per SIMD, split
-//   18:14 between the SIMD's older and younger wave, see wave_chunks), keeps
-//   its own (m, l, acc) and the waves are merged through LDS. With one split the workgroup writes the output,
+//   a contiguous range of 16-row chunks of one (sequence, q-head); each SIMD
+//   takes a quarter of the range, cut into ranges of its two waves (about
+//   18:14 between the SIMD's older and younger wave, the younger wave's last
+//   chunks a range of their own, see wave_segments); every range keeps its
+//   own (m, l, acc) and the ranges are merged through LDS in a fixed order.
+//   With one split the workgroup writes the output,
 //   otherwise (m, l, acc[D]) goes to the workspace and merge_kernel combines
 //   the splits with a log-sum-exp weighting.
 //
@@ -107,9 +109,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   __shared__ float q_s[D];
   __shared__ float p_s[WAVES][16];
   __shared__ float sz_s[WAVES][2 * D];
-  __shared__ float acc_s[WAVES][D];
-  __shared__ double m_s[WAVES];
-  __shared__ float l_s[WAVES];
+  // Partials of the wave_segments ranges (12 with eight waves).
+  static_assert(WAVES == 4 || WAVES == 8, "wave_segments assumes 4 or 8 waves");
+  constexpr int NS = WAVES > 4 ? WAVES + 4 : WAVES;
+  __shared__ float acc_s[NS][D];
+  __shared__ double m_s[NS];
+  __shared__ float l_s[NS];
   // With STEP: the open group's packed rows and scale/zero-point, as the
   // re-quantization left them (step_requant_slice).
   __shared__ uint16_t k_open[STEP ? kStepMaxGroup * D / 4 : 1];
@@ -140,8 +145,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   const int n_chunks = pages_of(a, T) * cpp;
   const int c_begin = split * a.chunks_per_split;
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
-  const WaveRange wr = wave_chunks(c_begin, c_end, w, WAVES);
-  const int wc0 = wr.c0, wc1 = wr.c1;
+  // The serving step's younger waves re-quantize first: the older waves take
+  // the last range of each SIMD (the same partials, computed by other waves).
+  const WaveSegs ws = wave_segments(c_begin, c_end, w, WAVES, append);
+  const int len1 = ws.p1 - ws.p0, len2 = ws.q1 - ws.q0, wlen = len1 + len2;
+  // The wave's i-th chunk.
+  auto cidx = [&](int i) { return i < len1 ? ws.p0 + i : ws.q0 + (i - len1); };
+  // Segment 1's partial is written when the loop reaches segment 2.
+  const bool seg_flush = ws.s2 >= 0 && len2 > 0;
 
   double m_run = -INFINITY;
   float l_lane = 0.f;
@@ -199,11 +210,33 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   // buffers swapped (a two-way unrolled ping-pong), so no register copy waits
   // on the prefetch. An empty chunk (page_lens 0) is loaded from row 0 of its
   // page and skipped.
-  int c = wc0;
+  int c = 0;
   ChunkMeta cm{}, nm{};
   U32x4 sz[G::SZL];
-  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, min(ci, wc1 - 1)); };
+  auto meta_at = [&](int ci) { return chunk_meta(a, b, T, cpp, cidx(min(ci, wlen - 1))); };
+  // Writes the wave's running partial (max logit, probability sum, weighted
+  // values, each reduced over the wave) to LDS slot `slot` and restarts the
+  // online softmax.
+  auto flush = [&](int slot) {
+    const float lw = allreduce_sum<1, 64>(l_lane);
+    float at[G::VCL];
+#pragma unroll
+    for (int k = 0; k < G::VCL; ++k) at[k] = allreduce_sum<G::VPR, 64>(acc[k]);
+    if (lane < G::VPR) {
+#pragma unroll
+      for (int k = 0; k < G::VCL; ++k) acc_s[slot][lane * G::VCL + k] = at[k];
+    }
+    if (lane == 0) {
+      m_s[slot] = m_run;
+      l_s[slot] = lw;
+    }
+    m_run = -INFINITY;
+    l_lane = 0.f;
+#pragma unroll
+    for (int k = 0; k < G::VCL; ++k) acc[k] = 0.f;
+  };
   auto step = [&](KVec<G::KW>* ck, U32x4* cv, KVec<G::KW>* nk, U32x4* nv) -> bool {
+    if (seg_flush && c == len1) flush(ws.s1);
     if (cm.group != cur_group) {
       const bool open = STEP && cm.group == open_g;
       // The open group's keys, scales and new value row are read from LDS
@@ -239,7 +272,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
       __builtin_amdgcn_wave_barrier();
     }
 
-    const bool last = c + 1 >= wc1;
+    const bool last = c + 1 >= wlen;
     // Unconditional loads: a conditional load here makes the wait counts at
     // the loop back-edge conservative (a full drain of the prefetch). On the
     // last step nm is the current chunk; with one valid row every lane reads
@@ -344,7 +377,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   static_assert(D <= NT, "one query element per thread");
   const float qv =
       (tid < D) ? load_elem(a.q, (int64_t)b * a.q_b + (int64_t)h * a.q_h + tid, a.q_dtype) : 0.f;
-  const bool has_work = c < wc1;
+  const bool has_work = wlen > 0;
   KVec<G::KW> ka[G::KLD], kb[G::KLD];
   U32x4 va[G::VLD], vb[G::VLD];
   // A re-quantizing wave (STEP) loads its first chunk after its quarter of
@@ -384,27 +417,19 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     }
   }
 
-  // Wave totals: l over all lanes, acc over the lanes holding the same channels.
-  const float lw = allreduce_sum<1, 64>(l_lane);
-#pragma unroll
-  for (int k = 0; k < G::VCL; ++k) acc[k] = allreduce_sum<G::VPR, 64>(acc[k]);
-  if (lane < G::VPR) {
-#pragma unroll
-    for (int k = 0; k < G::VCL; ++k) acc_s[w][lane * G::VCL + k] = acc[k];
-  }
-  if (lane == 0) {
-    m_s[w] = m_run;
-    l_s[w] = lw;
-  }
+  // The last segment's partial; a range that this wave owns but that is
+  // empty (C with no chunks) gets the empty partial.
+  flush(seg_flush ? ws.s2 : ws.s1);
+  if (ws.s2 >= 0 && !seg_flush) flush(ws.s2);
   __syncthreads();
 
   double ms = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < WAVES; ++i) ms = fmax(ms, m_s[i]);
-  float ew[WAVES];
+  for (int i = 0; i < NS; ++i) ms = fmax(ms, m_s[i]);
+  float ew[NS];
   float l = 0.f;
 #pragma unroll
-  for (int i = 0; i < WAVES; ++i) {
+  for (int i = 0; i < NS; ++i) {
     ew[i] = (m_s[i] == -INFINITY) ? 0.f : expf((float)(m_s[i] - ms));
     l = __builtin_fmaf(ew[i], l_s[i], l);
   }
@@ -412,7 +437,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   for (int d = tid; d < D; d += NT) {
     float o = 0.f;
 #pragma unroll
-    for (int i = 0; i < WAVES; ++i) o = __builtin_fmaf(ew[i], acc_s[i][d], o);
+    for (int i = 0; i < NS; ++i) o = __builtin_fmaf(ew[i], acc_s[i][d], o);
     if (a.final_out) {
       store_elem(a.out, (int64_t)b * a.o_b + (int64_t)h * a.o_h + d, a.out_dtype,
                  o / fmaxf(l, 1e-10f));

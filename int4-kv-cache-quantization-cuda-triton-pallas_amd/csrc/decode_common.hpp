@@ -176,6 +176,60 @@ __device__ __forceinline__ WaveRange wave_chunks(int begin, int end, int w, int 
   return r;
 }
 
+// The decode kernel's (decode_kernel) chunks of wave w of `waves` (4 or 8)
+// over the chunks [begin, end) of a split, as up to two segments, each with
+// an online-softmax partial of its own (LDS slot s1, and s2 when s2 >= 0).
+// SIMD s = w % 4 takes the same consecutive chunks [S, E) as in wave_chunks
+// (n of them). With four waves that is the wave's one segment (slot w). With
+// eight, [S, E) is cut into three ranges: A = the first (n * kFirstShare32 +
+// 16) / 32 chunks, C = the last (n * kTailShare32 + 16) / 32 of the rest, B
+// between; A's partial goes to slot s, B's to 4 + s, C's to 8 + s (12 slots,
+// merged in slot order). The older wave w < 4 takes A, the younger wave w + 4
+// takes B; C goes to the younger wave (then its segments B, C are contiguous)
+// unless `lend_tail`, when the older wave takes it after A. A wave's partial
+// for a range is the same whichever wave computes it, so the two assignments
+// give the same bits; the serving step (whose younger waves first
+// re-quantize the open group) lends C to the older waves.
+#ifndef FDI4_TAIL_SHARE32
+#define FDI4_TAIL_SHARE32 2
+#endif
+constexpr int kTailShare32 = FDI4_TAIL_SHARE32;
+
+struct WaveSegs {
+  int p0, p1;      // segment 1: chunks [p0, p1), partial in slot s1
+  int q0, q1;      // segment 2: chunks [q0, q1), partial in slot s2
+  int s1, s2;      // s2 < 0: no segment 2 (q0 == q1)
+};
+
+__device__ __forceinline__ WaveSegs wave_segments(int begin, int end, int w, int waves,
+                                                  bool lend_tail) {
+  const int span = max(end - begin, 0);
+  const int simds = min(waves, 4);
+  const int s = w % simds;
+  const int base = span / simds, rem = span - base * simds;
+  const int S = begin + s * base + min(s, rem);
+  const int n = base + (s < rem ? 1 : 0);
+  const int E = S + n;
+  WaveSegs r;
+  if (waves <= simds) {
+    r.p0 = S; r.p1 = E; r.q0 = r.q1 = E; r.s1 = w; r.s2 = -1;
+    return r;
+  }
+  const int first = (n * kFirstShare32 + 16) / 32;
+  const int tail = min((n * kTailShare32 + 16) / 32, n - first);
+  const int a1 = S + first, c0 = E - tail;
+  if (w < simds) {
+    r.p0 = S; r.p1 = a1; r.s1 = s;
+    if (lend_tail) { r.q0 = c0; r.q1 = E; } else { r.q0 = r.q1 = E; }
+  } else {
+    r.p0 = a1; r.p1 = c0; r.s1 = 4 + s;
+    if (lend_tail) { r.q0 = r.q1 = E; } else { r.q0 = c0; r.q1 = E; }
+  }
+  // C's partial is written by the wave that owns C, also when C is empty.
+  r.s2 = ((w >= simds) != lend_tail) ? 8 + s : -1;
+  return r;
+}
+
 // exp(x) for x <= ~0 in double: the exponent x*log2(e) is formed in double,
 // rounded once to float (relative 2^-24, so 6e-8 absolute where |x| < 1, where
 // the terms that matter lie) and raised with the hardware 2^y (v_exp_f32, ~1

@@ -47,22 +47,29 @@ def _same(a, b, what):
         assert torch.equal(getattr(a, name), getattr(b, name)), (what, name)
 
 
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("D,page_rows,group_rows,value_dtype,lens0", [
     (128, 16, 128, "float32", [126, 15, 250, 1]),
     (128, 16, 64, "float16", [62, 16, 0, 300]),
     (64, 32, 256, "bfloat16", [250, 31, 64, 5]),
     (256, 16, 128, "float32", [127, 200, 17, 40]),
     (128, 32, 256, "float16", [255, 1, 96, 130]),
+    # long enough that each SIMD's last chunks form a range of their own,
+    # which the step hands to the older wave of the SIMD (eight waves)
+    (128, 16, 128, "float32", [1023, 700, 517, 2047]),
+    (64, 16, 64, "bfloat16", [1500, 64, 900, 1279]),
 ])
-def test_fused_step_equals_three_launches(D, page_rows, group_rows, value_dtype, lens0):
+def test_fused_step_equals_three_launches(D, page_rows, group_rows, value_dtype, lens0, waves):
     import torch
     from flash_decode_int4 import capi
     B, H, steps = len(lens0), 2, 6
-    (new, old), g = _twins(B, H, D, lens0, page_rows, group_rows, value_dtype, 512, 31)
+    (new, old), g = _twins(B, H, D, lens0, page_rows, group_rows, value_dtype,
+                           max(512, max(lens0) + 64), 31)
     vdt = getattr(torch, value_dtype)
     for c in (new, old):
         c.reserve(B, steps)
-    with capi.tuning(decode_target_waves=1):        # one split: the one-launch step
+    # one split (the one-launch step), both workgroup sizes
+    with capi.tuning(decode_target_waves=1, decode_waves=waves):
         for i in range(steps):
             kn = torch.randn(B, H, D, device="cuda", generator=g)
             vn = torch.randn(B, H, D, device="cuda", generator=g).to(vdt)
