@@ -117,7 +117,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   __shared__ float l_s[NS];
   // With STEP: the open group's packed rows and scale/zero-point, as the
   // re-quantization left them (step_requant_slice).
-  __shared__ uint16_t k_open[STEP ? kStepMaxGroup * D / 4 : 1];
+  __shared__ __align__(16) uint16_t k_open[STEP ? kStepMaxGroup * D / 4 : 1];
   __shared__ float sz_open[STEP ? 2 * D : 1];
   __shared__ U32x4 v_open[STEP ? D * G::VEB / 16 : 1];
   // With STEP: each re-quantizing wave's copy of the group's page-table

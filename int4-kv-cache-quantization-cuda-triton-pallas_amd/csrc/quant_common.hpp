@@ -54,14 +54,15 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 // 0..rnew-1 from the staging rows through a range-checked buffer load, which
 // reads zeros past them without touching memory, replaced by the new row,
 // row rnew), per-channel min/max by a lane butterfly, the slice's scale and
-// zero-point, and the slice's two bytes of every packed row of the group. The
-// arithmetic is that of the grouped quantizer (quant_bin_rc, scale_zp), so
-// the stored bytes equal the append kernel's. The slice's share of the new
-// key row goes to the staging rows and its share of the new value row to the
-// value page. The group's packed rows (row r at byte r * D / 2), scale and
+// zero-point, and the slice's D / 8 bytes of every packed row of the group
+// (built in LDS, k_open, then stored with one store per row). The arithmetic
+// is that of the grouped quantizer (quant_bin_rc, scale_zp), so the stored
+// bytes equal the append kernel's. The slice's share of the new key row goes
+// to the staging rows and its share of the new value row to the value page.
+// The group's packed rows (row r at byte r * D / 2 of k_open), scale and
 // zero-point (scale of channel d at d, zero-point at D + d) and the new value
-// row are also written to the workgroup's LDS, k_open, sz_open and v_open;
-// the caller publishes them to the other waves once its LDS writes are done.
+// row are also left in the workgroup's LDS, k_open, sz_open and v_open; the
+// caller publishes them to the other waves once its LDS writes are done.
 // The stores to the cache are issued, not awaited: until the kernel ends the
 // workgroup reads the open group's keys and scales and the new value row
 // from LDS, never from the cache. pt_w: this wave's own LDS scratch of
@@ -190,9 +191,9 @@ __device__ __forceinline__ void step_requant_slice(const StepAppend& s, uint8_t*
   }
 
   // Bins of the valid rows: this lane's 4 channels of each of its rows, two
-  // bytes of the packed row, into k_open and the row's page. The last batch
-  // is still in registers; earlier ones (groups of more rows than one batch)
-  // are loaded again.
+  // bytes of the packed row, into k_open. The last batch is still in
+  // registers; earlier ones (groups of more rows than one batch) are loaded
+  // again.
 #pragma unroll 1
   for (int bt = nbu - 1; bt >= 0; --bt) {
     if (NBATCH > 1 && bt != nbu - 1) load_batch(bt);
@@ -208,11 +209,28 @@ __device__ __forceinline__ void step_requant_slice(const StepAppend& s, uint8_t*
         const uint16_t pk = (uint16_t)(unsigned)__builtin_fmaf(
             n3, 4096.0f, __builtin_fmaf(n2, 256.0f, __builtin_fmaf(n1, 16.0f, n0)));
         k_open[r * (D / 4) + ch / 4] = pk;
-        const int tok = r0 + r;
-        *reinterpret_cast<uint16_t*>(k_pages + (int64_t)pt_w[r / page_rows] * kp_page +
-                                     (int64_t)h * kp_head +
-                                     (int64_t)(tok % page_rows) * kp_row + ch / 2) = pk;
       }
+    }
+  }
+  // The slice's D / 8 bytes of every packed row, gathered from k_open: one
+  // store of up to 16 bytes per row and piece (lane j: row j, j + 64, ...),
+  // instead of one 2-byte store per lane and row.
+  constexpr int SB = D / 8;
+  constexpr int PB = SB < 16 ? SB : 16;
+  constexpr int PPR = SB / PB;
+  static_assert(PB == 8 || PB == 16, "piece");
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int j = lane; j < (rnew + 1) * PPR; j += 64) {
+    const int r = j / PPR, off = slice * SB + (j % PPR) * PB;
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(k_open) + r * (D / 2) + off;
+    uint8_t* dst = k_pages + (int64_t)pt_w[r / page_rows] * kp_page + (int64_t)h * kp_head +
+                   (int64_t)((r0 + r) % page_rows) * kp_row + off;
+    if constexpr (PB == 16) {
+      st16(dst, *reinterpret_cast<const U32x4*>(src));
+    } else {
+      *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
     }
   }
 }
