@@ -90,6 +90,18 @@ __device__ __forceinline__ void step_arrive(const DecodeArgs& a, int b, int T) {
   }
 }
 
+// One split's term of the log-sum-exp merge of an output element: split
+// maximum m (-inf: the split holds no rows and adds nothing), its sum of
+// probabilities lraw and weighted value acc, against the maximum ms over the
+// splits.
+__device__ __forceinline__ void merge_term(double m, double ms, float acc, double lraw, float& o,
+                                           float& l) {
+  if (m == -INFINITY) return;
+  const float e = expf((float)(m - ms));
+  o = __builtin_fmaf(e, acc, o);
+  l = __builtin_fmaf(e, (float)lraw, l);
+}
+
 template <int D, int VDT, int WAVES, bool STEP>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   using G = Geo<D, VDT>;
@@ -453,7 +465,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   if constexpr (STEP) step_arrive(a, b, T);
 }
 
-// Log-sum-exp merge of the split partials: grid (Hq, B), one thread per channel.
+// Log-sum-exp merge of the split partials: grid (Hq, B), one thread per
+// channel. Split s adds nothing when its maximum is -inf (no rows); the
+// others add exp(m_s - max) times their values and sums, in split order. Up
+// to eight splits every partial a thread needs is loaded in one round
+// (indices clamped to the last split, the extra loads unused); more splits
+// take the loop.
 template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ ws_acc,
                                                   const double* __restrict__ ws_ml, int hq,
@@ -462,14 +479,32 @@ __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ ws_a
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int64_t p0 = ((int64_t)b * hq + h) * splits;
   double ms = -INFINITY;
-  for (int s = 0; s < splits; ++s) ms = fmax(ms, ws_ml[2 * (p0 + s)]);
   float o = 0.f, l = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const double m = ws_ml[2 * (p0 + s)];
-    if (m == -INFINITY) continue;
-    const float e = expf((float)(m - ms));
-    o = __builtin_fmaf(e, ws_acc[(p0 + s) * D + d], o);
-    l = __builtin_fmaf(e, (float)ws_ml[2 * (p0 + s) + 1], l);
+  if (splits <= 8) {
+    double mv[8], lv[8];
+    float av[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t p = p0 + min(j, splits - 1);
+      mv[j] = ws_ml[2 * p];
+      lv[j] = ws_ml[2 * p + 1];
+      av[j] = ws_acc[p * D + d];
+    }
+    // Each value is used only under its split's condition; without this the
+    // compiler moves every load into its branch, one memory round per split.
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(av[j]));
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < splits) ms = fmax(ms, mv[j]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < splits) merge_term(mv[j], ms, av[j], lv[j], o, l);
+  } else {
+    for (int s = 0; s < splits; ++s) ms = fmax(ms, ws_ml[2 * (p0 + s)]);
+    for (int s = 0; s < splits; ++s)
+      merge_term(ws_ml[2 * (p0 + s)], ms, ws_acc[(p0 + s) * D + d], ws_ml[2 * (p0 + s) + 1], o,
+                 l);
   }
   store_elem(out, (int64_t)b * o_b + (int64_t)h * o_h + d, out_dtype, o / fmaxf(l, 1e-10f));
 }
