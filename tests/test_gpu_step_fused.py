@@ -5,7 +5,7 @@ workgroup barrier, while the other waves decode), decodes over the advanced
 length, and the last workgroup of a sequence advances its length. Checked bit for bit against the
 three-launch form (append kernel, a length increment, decode) on twin
 caches, over steps that cross page and group boundaries, for every value
-type, head_dim 64/128/256, page sizes 16/32 and groups 64/128/256; replayed
+type, head_dim 64/128/256, page sizes 2/8/16/32 and groups 64/128/256; replayed
 from a captured HIP graph; at a sequence already at the cache's capacity;
 and at the anchor size B8 H32 D128 from 2048 tokens."""
 
@@ -58,6 +58,9 @@ def _same(a, b, what):
     # which the step hands to the older wave of the SIMD (eight waves)
     (128, 16, 128, "float32", [1023, 700, 517, 2047]),
     (64, 16, 64, "bfloat16", [1500, 64, 900, 1279]),
+    # pages of 8 rows; pages of 2 rows, so a 256-row group spans 128 pages
+    (128, 8, 128, "bfloat16", [129, 7, 300, 64]),
+    (64, 2, 256, "float32", [255, 140, 3, 0]),
 ])
 def test_fused_step_equals_three_launches(D, page_rows, group_rows, value_dtype, lens0, waves):
     import torch
