@@ -109,6 +109,12 @@ def parse():
                    help="time the decode of the workload and nothing else (no other paths, "
                         "PMC or CPU legs): the command a rocprofv3 kernel trace of the "
                         "headline loop runs")
+    p.add_argument("--step-only", action="store_true",
+                   help="time the serving step (B8 H32 D128 around 2048 tokens, eager steps "
+                        "and the plain decode of the same cache) and nothing else, then run "
+                        "the 256 MiB calibration kernels; prints other_paths.decode_step "
+                        "without the graph figures (the command rocprofv3 --pmc passes over "
+                        "the step kernel run)")
     p.add_argument("--pmc-child", default="", help=argparse.SUPPRESS)
     return p.parse_args()
 
@@ -564,7 +570,7 @@ def time_other_paths(args):
     return out
 
 
-def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8):
+def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8, graphs=True):
     """The serving loop's step on the sequence cache (fp32 values, B sequences
     of H heads around T tokens): append one token per (sequence, kv-head),
     decode over the advanced lengths, advance them -- one launch when each
@@ -576,7 +582,7 @@ def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8):
     Python, one-step graph replays, and replays of a graph of `graph_steps`
     steps (the graph launch's own cost spread over them). Medians over the
     rounds, per step; `decode_us` is the plain decode of the same cache at T
-    tokens."""
+    tokens (graphs=False: the eager steps and that decode only)."""
     import torch
     from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
     G = 128
@@ -615,31 +621,40 @@ def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8):
     for _ in range(min(args.warmup, G)):
         cache.step(kn, vn, q)
     restore()
-    graph_1 = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph_1):
-        out_1 = cache.step(kn, vn, q)
-    graph_k = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph_k):
-        for _ in range(graph_steps):
-            out_k = cache.step(kn, vn, q)
+    graph_1 = graph_k = None
+    if graphs:
+        graph_1 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph_1):
+            out_1 = cache.step(kn, vn, q)
+        graph_k = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph_k):
+            for _ in range(graph_steps):
+                out_k = cache.step(kn, vn, q)
     eager, rep_1, rep_k = [], [], []
     for _ in range(rounds):
         restore()
         eager.append(timed(lambda: cache.step(kn, vn, q), G) / G)
-        restore()
-        rep_1.append(timed(graph_1.replay, G) / G)
-        restore()
-        rep_k.append(timed(graph_k.replay, G // graph_steps) / G)
-    ok = bool(torch.isfinite(out_1).all()) and bool(torch.isfinite(out_k).all())
+        if graphs:
+            restore()
+            rep_1.append(timed(graph_1.replay, G) / G)
+            restore()
+            rep_k.append(timed(graph_k.replay, G // graph_steps) / G)
     cache.sync_lengths()
     end_len = int(cache.lengths()[0])
+    if graphs:
+        ok = bool(torch.isfinite(out_1).all()) and bool(torch.isfinite(out_k).all())
+    else:
+        restore()
+        ok = bool(torch.isfinite(cache.step(kn, vn, q)).all())
     restore(T)
     dec = median([timed(lambda: cache.decode(q), 20) / 20 for _ in range(rounds)])
     res = {"workload": f"B{B} H{H} D{D}, fp32 values: append + decode + length advance per "
                        f"step, steps from {T0} to {T0 + G} tokens (one {G}-token scale group, "
                        f"mean {T - 0.5})",
-           "eager_us": round(median(eager), 3), "graph_replay_us": round(median(rep_1), 3),
-           f"graph_{graph_steps}_steps_replay_us_per_step": round(median(rep_k), 3),
+           "eager_us": round(median(eager), 3),
+           "graph_replay_us": round(median(rep_1), 3) if graphs else None,
+           f"graph_{graph_steps}_steps_replay_us_per_step":
+               round(median(rep_k), 3) if graphs else None,
            "decode_us": round(dec, 3), "rounds": rounds, "finite": ok,
            "final_length": end_len}
     del cache, graph_1, graph_k
@@ -796,8 +811,16 @@ def pmc_child(args):
     time_quantizer(sets, steps=3, warmup=1)
     del sets
     torch.cuda.empty_cache()
-    # Calibration kernels over 256 MiB of float32: a fill (writes only), a sum
-    # (reads only) and an elementwise copy (reads and writes).
+    calibration_kernels()
+    time_fake_quant(steps=2, warmup=1)
+    print(json.dumps({"splits": r["splits"]}))
+
+
+def calibration_kernels():
+    """Kernels over 256 MiB of float32 whose PMC readings give bytes per
+    counter unit: a fill (writes only), a sum (reads only) and an elementwise
+    copy (reads and writes), three launches each."""
+    import torch
     a = torch.empty(64 * 2 ** 20, dtype=torch.float32, device="cuda")
     b = torch.empty_like(a)
     for _ in range(3):
@@ -809,8 +832,6 @@ def pmc_child(args):
     torch.cuda.synchronize()
     del a, b
     torch.cuda.empty_cache()
-    time_fake_quant(steps=2, warmup=1)
-    print(json.dumps({"splits": r["splits"]}))
 
 
 def pmc_traffic(args):
@@ -910,6 +931,11 @@ def main():
         print("bench.py: the HIP extension or the GPU is unavailable: "
               f"{ops.backend_status()}", file=sys.stderr)
         sys.exit(1)
+    if args.step_only:
+        res = time_decode_step(args, graphs=False)
+        calibration_kernels()
+        print(json.dumps({"decode_step": res}))
+        return
 
     sets, set_bytes = build_sets(args.workload, args.value_dtype, seq_lens=workload_lens(args))
     w0 = sets[0]["w"]
