@@ -8,17 +8,25 @@ groups, fp32 values), plus the grouped quantizer's GB/s.
 A step is one decode of the whole batch on inputs already resident in HBM:
 the decode kernel (plus the split merge when the library splits the
 sequences). Input sets are rotated so their total exceeds twice the 256 MB
-Infinity Cache (nothing is served from the cache across steps). The quantizer
-is timed in its own loop over the same rotation. One pair of HIP events on the
-launch stream brackets K back-to-back launches (per-launch markers would add
-their own time to the GPU timeline); wall clock brackets the K steps too. Bytes are algorithmic (valid tokens only): packed K T*D/2, V
-T*D*4, scale and zero-point ceil(T/128)*D*8 per (sequence, head), the page
-table, sequence lengths, q and the output.
+Infinity Cache (nothing is served from the cache across steps). Bytes are
+algorithmic (valid tokens only): packed K T*D/2, V T*D*4, scale and
+zero-point ceil(T/128)*D*8 per (sequence, head), the page table, sequence
+lengths, q and the output.
+
+Clocks. `value` and `ms_per_step` come from the wall clock around exactly K
+(--steps) back-to-back steps, synchronized on both sides (the step contract;
+host launch cost included). `decode_us` and the roofline figure come from
+HIP events on the launch stream around a steady-state window of at least 400
+back-to-back launches (20 blocks, an event between blocks, no host
+synchronization inside the window, whatever --steps is); `decode_us_median`
+is the median over the window's blocks. `roofline.trace_*` are the decode
+kernel's per-dispatch durations over the same window, from a rocprofv3
+--kernel-trace child process (`--no-trace` skips it). The quantizers and the
+other decode paths are timed over windows of the same shape.
 
 hbm_probe reports what a plain torch elementwise kernel reading and writing
 1 GiB reaches on the same box, beside the 8 TB/s specification used as the
-roofline peak; decode_us_median and quantizer_us_median are medians over
-blocks of 10 back-to-back launches.
+roofline peak.
 
 reference_config times the drop-in API (prepare_flash_decode_hip().run()) on
 the reference's own benchmark semantics, beside the reference's published
@@ -27,7 +35,8 @@ CUDA time for it on other hardware (context, not vs_baseline).
 reference_quantizer times the drop-in quantize_int4 (one scale group over all
 rows of a [rows, 128] array, unpacked bins) at the two row counts the
 reference publishes CUDA times for, beside those times; the CPU leg checks its
-bins, scales and zero-points bit for bit against the oracle.
+bins, scales and zero-points bit for bit against the oracle, and the PMC
+children give the HBM traffic of its kernels.
 
 other_paths times the decode with fp16 value pages at the anchor shape and with
 grouped-query heads (B8, 8 kv-heads, 32 q-heads, 8192 tokens), and the serving
@@ -55,14 +64,15 @@ must be given when this script itself runs under rocprofv3).
 
 checks.seq_len_plus_1 re-runs the decode with every length + 1 (pages and
 groups one row into fresh ones); its "interleaved" record times the workload
-and the + 1 lengths in alternating blocks, so the two figures share clocks
-and memory state.
+and the + 1 lengths in alternating blocks of back-to-back launches (no host
+synchronization between blocks), so the two figures share clocks and memory
+state.
 
-Prints ONE JSON line. Options: --workload (anchor, sweep_512 ... llama,
-ragged), --tokens (every sequence at that length), --splits, --value-dtype
-float16|bfloat16, --no-cpu, --no-pmc, --decode-only (the decode timing
-alone: the command whose rocprofv3 kernel trace is the profile of the
-headline loop).
+Prints ONE JSON line on stdout (progress lines go to stderr). Options:
+--workload (anchor, sweep_512 ... llama, ragged), --tokens (every sequence at
+that length), --splits, --value-dtype float16|bfloat16, --no-cpu, --no-pmc,
+--no-trace (both required when this script itself runs under rocprofv3),
+--decode-only (the decode timing alone).
 """
 
 import argparse
@@ -115,8 +125,17 @@ def parse():
                         "the 256 MiB calibration kernels; prints other_paths.decode_step "
                         "without the graph figures (the command rocprofv3 --pmc passes over "
                         "the step kernel run)")
+    p.add_argument("--no-trace", action="store_true",
+                   help="skip the rocprofv3 --kernel-trace child of the headline window "
+                        "(required under rocprofv3)")
     p.add_argument("--pmc-child", default="", help=argparse.SUPPRESS)
+    p.add_argument("--trace-child", action="store_true", help=argparse.SUPPRESS)
     return p.parse_args()
+
+
+def progress(msg):
+    """A progress line on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def workload_lens(args):
@@ -231,17 +250,12 @@ def time_reference_quantizer(steps, warmup):
         host[f"rows_{rows}x{C}"] = (sets[0].cpu().numpy(), calls[0]())
         for i in range(warmup):
             calls[i % n_sets].run()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for i in range(steps):
-            calls[i % n_sets].run()
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / steps
+        nb, blk = window_shape(steps)
+        us, us_med, _ = window_us(lambda i: calls[i % n_sets].run(), nb, blk)
         nbytes = in_bytes + rows * C + 2 * C * 4
         out[f"rows_{rows}x{C}"] = {
-            "us": round(us, 3), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "us": round(us, 3), "us_median": round(us_med, 3), "bytes": nbytes,
+            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
             "input_sets": n_sets, "reference_cuda_h100_us": ref_us}
         del sets, calls
         torch.cuda.empty_cache()
@@ -264,22 +278,46 @@ def cpu_check_reference_quantizer(host):
     return res
 
 
-def blocked_median_us(fn, n, block=10):
-    """Median over n // block blocks of the per-launch time of `block`
-    back-to-back launches (one event pair per block; each block starts from an
-    idle GPU, so this runs a little above the long-run mean)."""
+#: The steady-state window of the roofline figure: WINDOW_BLOCKS blocks of
+#: back-to-back launches (at least WINDOW_MIN launches in all, more when
+#: --steps asks for more), one HIP event between blocks and no host
+#: synchronization inside the window.
+WINDOW_BLOCKS = 20
+WINDOW_MIN = 400
+
+
+def window_shape(steps):
+    """(blocks, launches per block) of the steady-state window."""
+    per = max(WINDOW_MIN, steps)
+    return WINDOW_BLOCKS, -(-per // WINDOW_BLOCKS)
+
+
+def window_us(fn, blocks, block, start=0):
+    """Back-to-back launches in `blocks` blocks of `block`, one event on the
+    launch stream before the first block and after every block, one
+    synchronize at the end (the GPU never idles inside the window). Returns
+    (mean per launch over the window, median over the blocks of the
+    per-launch time of a block, launches)."""
     import torch
-    out = []
-    for j in range(max(1, n // block)):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for i in range(block):
-            fn(j * block + i)
-        e1.record()
-        torch.cuda.synchronize()
-        out.append(e0.elapsed_time(e1) * 1e3 / block)
-    return median(out)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(blocks + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    k = start
+    for j in range(blocks):
+        for _ in range(block):
+            fn(k)
+            k += 1
+        ev[j + 1].record()
+    torch.cuda.synchronize()
+    per = [ev[j].elapsed_time(ev[j + 1]) * 1e3 / block for j in range(blocks)]
+    return ev[0].elapsed_time(ev[blocks]) * 1e3 / (blocks * block), median(per), blocks * block
+
+
+def blocked_median_us(fn, n, block=10):
+    """Median over the blocks of a window of back-to-back launches (at least
+    20 blocks of `block` launches, more when n asks for more), with no host
+    synchronization between blocks."""
+    return window_us(fn, max(20, -(-n // block)), block)[1]
 
 
 def hbm_probes():
@@ -346,21 +384,22 @@ def decode_launchers(sets, splits):
 
 def interleaved_us(fa, fb, rounds=10, block=20):
     """Per-launch time of two launch sequences measured in alternating blocks
-    (A, B, A, B, ...; one event pair per block of `block` back-to-back
-    launches, a synchronize before each block), so both see the same clocks
-    and memory state; returns the two medians over the rounds."""
+    (A, B, A, B, ...) of `block` back-to-back launches, one event between
+    blocks and one synchronize at the end, so both see the same clocks and
+    memory state and the GPU never idles between blocks; returns the two
+    medians over the rounds."""
     import torch
-    ta, tb = [], []
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * rounds + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
     for r in range(rounds):
-        for fn, out in ((fa, ta), (fb, tb)):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            e0.record()
+        for j, fn in enumerate((fa, fb)):
             for i in range(block):
                 fn(r * block + i)
-            e1.record()
-            torch.cuda.synchronize()
-            out.append(e0.elapsed_time(e1) * 1e3 / block)
+            ev[2 * r + j + 1].record()
+    torch.cuda.synchronize()
+    ta = [ev[2 * r].elapsed_time(ev[2 * r + 1]) * 1e3 / block for r in range(rounds)]
+    tb = [ev[2 * r + 1].elapsed_time(ev[2 * r + 2]) * 1e3 / block for r in range(rounds)]
     return median(ta), median(tb)
 
 
@@ -385,21 +424,24 @@ def time_decode(sets, splits, steps, warmup):
     for i in range(warmup):
         step(i)
     out, wall, step_us = timed(step, steps)
-    step_median = blocked_median_us(step, steps)
+    nb, blk = window_shape(steps)
+    win_us, win_median, win_n = window_us(step, nb, blk, start=steps)
     if S == 1:
-        dec_us = step_us
+        dec_us, dec_median = win_us, win_median
     else:
         for i in range(warmup):
             decode_only(i)
-        _, _, dec_us = timed(decode_only, steps)
-    return dict(splits=S, wall_s=wall, step_us=step_us, step_median_us=step_median,
-                decode_us=dec_us,
-                merge_us=max(step_us - dec_us, 0.0), last_out=out,
+        dec_us, dec_median, _ = window_us(decode_only, nb, blk)
+    return dict(splits=S, wall_s=wall, step_us=step_us, window_us=win_us,
+                step_median_us=win_median, window_launches=win_n, window_blocks=nb,
+                decode_us=dec_us, decode_median_us=dec_median,
+                merge_us=max(win_us - dec_us, 0.0), last_out=out,
                 last_set=(steps - 1) % len(sets))
 
 
 def time_quantizer(sets, steps, warmup):
-    import torch
+    """Grouped quantizer over the rotated input sets: (mean per launch over a
+    steady-state window, median over the window's blocks)."""
     from flash_decode_int4 import ops
     g = sets[0]["w"]["group_rows"]
 
@@ -409,14 +451,9 @@ def time_quantizer(sets, steps, warmup):
 
     for i in range(warmup):
         q(i)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for i in range(steps):
-        q(i)
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / steps, blocked_median_us(q, steps)
+    nb, blk = window_shape(steps)
+    mean, med, _ = window_us(q, nb, blk)
+    return mean, med
 
 
 def time_append(w, value_dtype, steps, warmup):
@@ -561,9 +598,10 @@ def time_other_paths(args):
             "workload": f"{name}: B{w['batch']} Hkv{w['heads']} Hq{w['q_heads']} D{w['head_dim']} "
                         f"T{int(max(w['seq_lens']))}, {vdt} values",
             "kernel": decode_kernel_label(w, vdt), "num_splits": r["splits"],
-            "bytes": nbytes, "decode_us": round(r["step_us"], 3),
-            "gbs": round(nbytes / (r["step_us"] * 1e-6) / 1e9, 1),
-            "hbm_frac": round(nbytes / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes": nbytes, "decode_us": round(r["window_us"], 3),
+            "decode_us_median": round(r["step_median_us"], 3),
+            "gbs": round(nbytes / (r["window_us"] * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (r["window_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "finite": bool(torch.isfinite(r["last_out"]).all())}
         del sets
         torch.cuda.empty_cache()
@@ -813,6 +851,7 @@ def pmc_child(args):
     torch.cuda.empty_cache()
     calibration_kernels()
     time_fake_quant(steps=2, warmup=1)
+    time_reference_quantizer(steps=3, warmup=1)
     print(json.dumps({"splits": r["splits"]}))
 
 
@@ -874,11 +913,21 @@ def pmc_traffic(args):
         qz = values(lambda k: "quantize_paged_kernel" in k)
         fq = {name: values(lambda k, t=tag: "fake_quant_kernel" in k and t in k)
               for name, tag in (("harness_window_f16", "F16Key"), ("decode_keys_f32", "F32Key"))}
+        # The 2-D quantizer's kernels (fdi4::rows_*) by grid, then kernel: at
+        # both row counts a call is two launches on the same (channel slices,
+        # row tiles) grid, which grows with the rows.
+        rq = {}
+        for row in rows:
+            k = row.get("Kernel_Name", "")
+            if "fdi4::rows_" in k and row.get("Counter_Name") == counter:
+                name = k.split("fdi4::", 1)[1].split("(")[0]
+                rq.setdefault(int(row["Grid_Size"]), {}).setdefault(name, []).append(
+                    float(row["Counter_Value"]))
         shutil.rmtree(d, ignore_errors=True)
         if not dec or not cal or not cpy:
             return None, f"no {counter} rows for the decode or calibration kernels"
         out[counter] = (median(dec), max(cal), {k: median(v) for k, v in fq.items() if v},
-                        max(cpy), median(qz) if qz else None)
+                        max(cpy), median(qz) if qz else None, rq)
     # Each calibration kernel moves 256 MiB in the counted direction: the
     # factor converts counter units to bytes. The copy's factors are reported
     # beside them (its reads can include line fills for its writes).
@@ -892,11 +941,80 @@ def pmc_traffic(args):
     if out["FETCH_SIZE"][4] is not None and out["WRITE_SIZE"][4] is not None:
         quant = {"fetch_bytes": out["FETCH_SIZE"][4] * ff,
                  "write_bytes": out["WRITE_SIZE"][4] * wf}
+    # Per row count of the reference quantizer (the smaller grid is the
+    # 2048-row call), the medians of the call's kernels summed.
+    ref_q = {}
+    for counter, factor in (("FETCH_SIZE", ff), ("WRITE_SIZE", wf)):
+        by_grid = out[counter][5]
+        for i, g in enumerate(sorted(by_grid)[:2]):
+            rec = ref_q.setdefault(f"rows_{(2048, 32768)[i]}x128", {})
+            key = "fetch_bytes" if counter == "FETCH_SIZE" else "write_bytes"
+            rec[key] = sum(median(v) for v in by_grid[g].values()) * factor
+            rec["kernels"] = sorted(by_grid[g])
     return {"fetch_bytes": out["FETCH_SIZE"][0] * ff, "write_bytes": out["WRITE_SIZE"][0] * wf,
             "fetch_factor_bytes_per_unit": ff, "write_factor_bytes_per_unit": wf,
             "copy_fetch_factor_bytes_per_unit": cal_bytes / out["FETCH_SIZE"][3],
             "copy_write_factor_bytes_per_unit": cal_bytes / out["WRITE_SIZE"][3],
-            "fake_quant": fake, "quantizer": quant}, None
+            "fake_quant": fake, "quantizer": quant, "reference_quantizer": ref_q}, None
+
+
+def trace_child(args):
+    """The headline's decode window alone, for a rocprofv3 --kernel-trace
+    child: the same input sets, warmup, then the steady-state window of the
+    decode kernel (window_shape(--steps)); prints its own event figures."""
+    sets, _ = build_sets(args.workload, args.value_dtype, seq_lens=workload_lens(args))
+    S, step, decode_only = decode_launchers(sets, args.splits)
+    fn = step if S == 1 else decode_only
+    for i in range(args.warmup):
+        fn(i)
+    nb, blk = window_shape(args.steps)
+    mean, med, n = window_us(fn, nb, blk)
+    print(json.dumps({"splits": S, "window_launches": n, "event_us": mean,
+                      "event_median_us": med}), flush=True)
+
+
+def trace_window(args):
+    """Per-dispatch durations of the decode kernel over the steady-state
+    window, from a rocprofv3 --kernel-trace run of trace_child: the last
+    window_launches dispatches of the decode kernel (the warmup ones before
+    them are dropped)."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not found"
+    import csv
+    d = tempfile.mkdtemp(prefix="fdi4_trace_")
+    cmd = [exe, "--kernel-trace", "--stats", "-d", d, "-o", "trace", "--output-format", "csv",
+           "--", sys.executable, os.path.abspath(__file__), "--workload", args.workload,
+           "--tokens", str(args.tokens), "--splits", str(args.splits),
+           "--value-dtype", args.value_dtype, "--steps", str(args.steps),
+           "--warmup", str(args.warmup), "--trace-child"]
+    try:
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                           timeout=240, check=False)
+    except subprocess.TimeoutExpired:
+        shutil.rmtree(d, ignore_errors=True)
+        return None, "rocprofv3 --kernel-trace timed out"
+    child = None
+    for line in r.stdout.splitlines():
+        if line.startswith("{"):
+            child = json.loads(line)
+    rows = []
+    for dirpath, _, files in os.walk(d):
+        for f in files:
+            if f.endswith("kernel_trace.csv"):
+                with open(os.path.join(dirpath, f)) as fh:
+                    rows += list(csv.DictReader(fh))
+    shutil.rmtree(d, ignore_errors=True)
+    if child is None:
+        return None, f"trace child printed no result (rc {r.returncode})"
+    dec = sorted((int(x["Start_Timestamp"]), int(x["End_Timestamp"])) for x in rows
+                 if any(f"{n}<" in x.get("Kernel_Name", "") for n in DECODE_KERNELS))
+    n = int(child["window_launches"])
+    if len(dec) < n:
+        return None, f"{len(dec)} decode dispatches in the trace, {n} expected"
+    durs = [(e - b) * 1e-3 for b, e in dec[-n:]]
+    return {"trace_mean_us": sum(durs) / n, "trace_median_us": median(durs),
+            "trace_dispatches": n, "child_event_us": child["event_us"]}, None
 
 
 def decode_kernel_label(w, value_dtype):
@@ -925,6 +1043,9 @@ def main():
     if args.pmc_child:
         pmc_child(args)
         return
+    if args.trace_child:
+        trace_child(args)
+        return
     import torch
     from flash_decode_int4 import ops, workloads
     if not ops.HAS_HIP:
@@ -937,6 +1058,7 @@ def main():
         print(json.dumps({"decode_step": res}))
         return
 
+    progress(f"building the {args.workload} input sets")
     sets, set_bytes = build_sets(args.workload, args.value_dtype, seq_lens=workload_lens(args))
     w0 = sets[0]["w"]
     vbytes = 4 if args.value_dtype == "float32" else 2
@@ -954,8 +1076,9 @@ def main():
               file=sys.stderr)
         sys.exit(1)
 
+    progress("timing the decode")
     res = time_decode(sets, args.splits, args.steps, args.warmup)
-    dec_us, mrg_us, step_us = res["decode_us"], res["merge_us"], res["step_us"]
+    dec_us, mrg_us, win_us = res["decode_us"], res["merge_us"], res["window_us"]
     ms_per_step = res["wall_s"] / args.steps * 1e3
     line = {
         "metric": METRIC,
@@ -985,11 +1108,21 @@ def main():
             "group_rows": w0["group_rows"], "num_splits": res["splits"],
             "input_sets": len(sets), "bytes_per_step": set_bytes,
         },
-        "decode_us": round(step_us, 3),
+        "clocks": {
+            "value": f"wall clock around the {args.steps} timed steps (synchronize on both "
+                     "sides; host launch cost included)",
+            "decode_us": f"HIP events on the launch stream around a steady-state window of "
+                         f"{res['window_launches']} back-to-back steps "
+                         f"({res['window_blocks']} blocks, no host synchronization inside)",
+            "decode_us_median": "median over the window's blocks of the per-step time",
+            "decode_us_timed_loop": f"HIP events around the {args.steps} timed steps",
+        },
+        "decode_us": round(win_us, 3),
         "decode_us_median": round(res["step_median_us"], 3),
+        "decode_us_timed_loop": round(res["step_us"], 3),
         "decode_kernel_us": round(dec_us, 3),
         "merge_us": round(mrg_us, 3),
-        "hbm_frac": round(set_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "hbm_frac": round(set_bytes / (win_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
     }
     roofline = {
         "bound": "hbm",
@@ -999,18 +1132,42 @@ def main():
         "frac": round(set_bytes / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "traffic": None,
         "kernel": decode_kernel_label(w0, args.value_dtype),
+        "clock": (f"HIP events on the launch stream, mean over a steady-state window of "
+                  f"{res['window_launches']} back-to-back launches of the decode kernel"),
+        "window_launches": res["window_launches"],
+        "kernel_us": round(dec_us, 3),
+        "kernel_us_median": round(res["decode_median_us"], 3),
     }
     if args.decode_only:
         line["roofline"] = roofline
         print(json.dumps(line), flush=True)
         return
+    if not args.no_trace:
+        progress("rocprofv3 --kernel-trace child of the decode window")
+        tr, err = trace_window(args)
+        if tr is not None:
+            roofline.update({
+                "trace_mean_us": round(tr["trace_mean_us"], 3),
+                "trace_median_us": round(tr["trace_median_us"], 3),
+                "trace_dispatches": tr["trace_dispatches"],
+                "trace_frac": round(set_bytes / (tr["trace_mean_us"] * 1e-6) / 1e9
+                                    / HBM_PEAK_GBS, 4),
+                "trace_child_event_us": round(tr["child_event_us"], 3),
+                "trace_note": "per-dispatch kernel durations (rocprofv3 --kernel-trace) of the "
+                              "same window run in a child process; the event figure includes "
+                              "the gaps between back-to-back dispatches, the trace figure "
+                              "does not"})
+        else:
+            roofline["trace_error"] = err
 
+    progress("timing the quantizer, append, reference semantics and fake quantization")
     qt, qt_median = time_quantizer(sets, args.steps, args.warmup)
     app = time_append(w0, args.value_dtype, args.steps, args.warmup)
     probe = hbm_probes()
     refcfg = time_reference_config(args.steps, args.warmup)
     refq, refq_host = time_reference_quantizer(args.steps, args.warmup)
     fq = time_fake_quant(args.steps, args.warmup)
+    progress("timing the other decode paths and the serving step")
     other = time_other_paths(args)
     other["decode_step"] = time_decode_step(args)
     other["decode_step_small"] = time_decode_step(args, B=1, H=8, D=128, T=1024)
@@ -1020,6 +1177,7 @@ def main():
     # a fresh group; the output must be finite and the rate must hold.
     odd_lens = w0["seq_lens"] + 1
     odd_sets, odd_bytes = build_sets(args.workload, args.value_dtype, seq_lens=odd_lens)
+    progress("seq_len + 1 check")
     odd = time_decode(odd_sets, args.splits, max(args.steps // 2, 5), args.warmup)
     odd_ok = bool(torch.isfinite(odd["last_out"]).all())
     # The two lengths timed in alternating blocks (the same clocks and memory
@@ -1045,19 +1203,29 @@ def main():
             "split_invariance_max_abs": gate,
             "seq_len_plus_1": {
                 "pass": odd_ok, "max_tokens": int(odd_lens.max()),
-                "decode_us": round(odd["step_us"], 3),
-                "hbm_frac": round(odd_bytes / (odd["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "decode_us": round(odd["window_us"], 3),
+                "hbm_frac": round(odd_bytes / (odd["window_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                  4),
                 "interleaved": {"anchor_us": round(base_us, 3), "plus_1_us": round(odd_us, 3),
                                 "ratio": round(odd_us / base_us, 4), "rounds": 10,
-                                "launches_per_block": 20}},
+                                "launches_per_block": 20,
+                                "anchor_vs_headline": round(base_us / win_us, 4)}},
         },
         "roofline": roofline,
     })
     if not args.no_pmc:
+        progress("rocprofv3 --pmc children (FETCH_SIZE, WRITE_SIZE)")
         traffic, err = pmc_traffic(args)
         if traffic is not None:
             fake = traffic.pop("fake_quant")
             quant = traffic.pop("quantizer")
+            for name, t in traffic.pop("reference_quantizer").items():
+                rec = line["reference_quantizer"].get(name)
+                if rec is None or "fetch_bytes" not in t or "write_bytes" not in t:
+                    continue
+                rec["traffic"] = round(t["fetch_bytes"] + t["write_bytes"])
+                rec["traffic_vs_algorithmic"] = round(rec["traffic"] / rec["bytes"], 4)
+                rec["traffic_kernels"] = t["kernels"]
             if quant is not None:
                 qt_bytes = round(quant["fetch_bytes"] + quant["write_bytes"])
                 line["quantizer_traffic"] = qt_bytes
@@ -1071,6 +1239,7 @@ def main():
         else:
             line["roofline"]["traffic_error"] = err
     if not args.no_cpu:
+        progress("CPU baseline (NumPy oracle)")
         st = sets[res["last_set"]]
         base, parity = cpu_baseline(st, res["last_out"], args.cpu_runs, vbytes)
         line["cpu_baseline"] = base

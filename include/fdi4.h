@@ -268,9 +268,13 @@ int fdi4_decode_paged_advance(const void* query, int query_dtype, int batch, int
  * of every sequence b < batch (k_new float32 and v_new in the cache's value
  * type, [batch, num_kv_heads, head_dim] with element strides; the staging
  * rows k_stage as in fdi4_append_paged), attend with query over the t + 1
- * rows, and advance cache->seq_lens[b] to t + 1 (t when the sequence is
- * already at the cache's capacity). The result equals fdi4_append_paged,
- * a length increment and fdi4_decode_paged_ex, bit for bit.
+ * rows, and advance cache->seq_lens[b] to t + 1. A length outside
+ * [0, capacity) (capacity = max_pages * page_rows; a sequence already full,
+ * or a corrupt length) appends nothing, stays as it is, and the decode
+ * attends over it clamped to [0, capacity]. The result equals
+ * fdi4_append_paged, that length update and fdi4_decode_paged_ex, bit for
+ * bit. Every argument is checked before anything is enqueued: a rejected
+ * call (hipErrorInvalidValue) leaves the cache unchanged.
  * When each (sequence, kv-head) is one decode workgroup (num_q_heads ==
  * num_kv_heads and a single split) this is ONE launch: every workgroup
  * appends its own token and re-quantizes the open group before it decodes,
@@ -316,7 +320,10 @@ int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,
 /* fdi4_decode_paged without a workspace argument and without any allocation:
  * with more than one split the partials go to a static device array of
  * FDI4_NOALLOC_SCRATCH_BYTES that the library holds on each GPU (its address
- * is looked up on the first call on a device). A call whose partials would
+ * is looked up, with hipGetSymbolAddress, on the first multi-split call on a
+ * device: make that call once eagerly, outside any HIP graph capture, before
+ * capturing the entry point; later calls only enqueue kernels and can be
+ * captured). A call whose partials would
  * exceed the array returns hipErrorInvalidValue before any device work. The
  * caller still passes the inputs and the output. Calls that overlap on one GPU
  * (concurrent streams, or threads) share the array and race; serialize them.
@@ -363,6 +370,21 @@ int fdi4_fake_quantize(const void* k, int key_dtype, int batch, int heads, int s
                        int64_t k_row_stride, void* out, int64_t out_batch_stride,
                        int64_t out_head_stride, int64_t out_row_stride, int block_size,
                        int rounding, int scale_op, hipStream_t stream);
+
+/* Dequantization of stored INT4 values: out[r, c] = q*s - zp*s in float32
+ * (two rounded products, then a rounded subtraction) with s = scale[r *
+ * s_row_stride + c * s_channel_stride] and zp at the same offset: strides
+ * (0, 1) for per-channel scales [num_channels], (1, 0) for per-row scales
+ * [rows], (num_channels, 1) for one scale per element. q is one value per
+ * byte (the whole byte is the value) or, with packed != 0, two per byte
+ * (channel c in the low nibble of byte c/2 when c is even, the high nibble
+ * when odd); row strides in bytes (q) and elements (out). Bit-exact with the
+ * reference's dequantize_int4_ref (src/quantize_int4_ref.py:87-136), which
+ * the decode kernels fuse into their logits instead. */
+int fdi4_dequantize_int4(const uint8_t* q, int64_t rows, int num_channels, int64_t q_row_stride,
+                         int packed, const float* scale, const float* zp,
+                         int64_t s_row_stride, int64_t s_channel_stride, float* out,
+                         int64_t out_row_stride, hipStream_t stream);
 
 /* Device nibble packing: out[r, j] = q[r, 2j] | q[r, 2j+1] << 4 for
  * j < ceil(C/2) (odd C zero-padded), zero for ceil(C/2) <= j < out_cols.

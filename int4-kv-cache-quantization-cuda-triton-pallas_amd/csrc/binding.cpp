@@ -612,6 +612,40 @@ torch::Tensor pack_int4(torch::Tensor q, int64_t out_cols) {
   return out;
 }
 
+// Dequantization of stored INT4 values q [rows, bytes] (one value per byte,
+// or two nibbles per byte when packed) with scale / zp viewed as [rows,
+// num_channels] through their strides (0 for a broadcast axis; the two must
+// share strides): float32 [rows, num_channels] = q*s - zp*s.
+torch::Tensor dequantize_int4(torch::Tensor q, torch::Tensor scale, torch::Tensor zp,
+                              int64_t num_channels, bool packed) {
+  CHECK_DEV(q);
+  CHECK_DEV(scale);
+  CHECK_DEV(zp);
+  CHECK_SAME_DEVICE(q, scale);
+  CHECK_SAME_DEVICE(q, zp);
+  TORCH_CHECK(q.scalar_type() == torch::kUInt8 && q.dim() == 2 && q.stride(1) == 1,
+              "q must be uint8 [rows, bytes] with contiguous rows");
+  const int64_t rows = q.size(0);
+  TORCH_CHECK(num_channels >= 1 && num_channels <= INT32_MAX, "num_channels must be >= 1");
+  TORCH_CHECK(q.size(1) == (packed ? (num_channels + 1) / 2 : num_channels),
+              "q has ", q.size(1), " bytes per row for ", num_channels,
+              packed ? " packed channels" : " channels");
+  TORCH_CHECK(scale.scalar_type() == torch::kFloat32 && zp.scalar_type() == torch::kFloat32,
+              "scale and zp must be float32");
+  TORCH_CHECK(scale.dim() == 2 && scale.size(0) == rows && scale.size(1) == num_channels &&
+                  zp.sizes() == scale.sizes() && zp.strides() == scale.strides(),
+              "scale and zp must be [rows, num_channels] views with the same strides");
+  TORCH_CHECK(scale.stride(0) >= 0 && scale.stride(1) >= 0, "negative scale strides");
+  const DeviceGuard guard(q.device());
+  auto out = torch::empty({rows, num_channels}, q.options().dtype(torch::kFloat32));
+  check_rc(fdi4_dequantize_int4(q.data_ptr<uint8_t>(), rows, (int)num_channels, q.stride(0),
+                                packed ? 1 : 0, scale.data_ptr<float>(), zp.data_ptr<float>(),
+                                scale.stride(0), scale.stride(1), out.data_ptr<float>(),
+                                num_channels, stream()),
+           "dequantize_int4");
+  return out;
+}
+
 // INT4 quantize-dequantize of keys [batch, heads, seq, head_dim] into `out`
 // (same dtype and shape; see fdi4_fake_quantize). rounding: 0 half-up, 1
 // half-even; scale_op: 0 divide, 1 reciprocal.
@@ -669,6 +703,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_partials_bytes", &decode_partials_bytes, "Bytes of the split partials");
   m.def("decode_num_splits", &decode_num_splits, "Split count chosen for a decode shape");
   m.def("pack_int4", &pack_int4, "Device nibble packing (HIP)");
+  m.def("dequantize_int4", &dequantize_int4, "Dequantization of stored INT4 values (HIP)");
   m.def("fake_quantize", &fake_quantize, "INT4 quantize-dequantize of keys in blocks (HIP)");
   m.def("abi_version", &fdi4_abi_version, "C ABI version of the loaded libfdi4");
 }

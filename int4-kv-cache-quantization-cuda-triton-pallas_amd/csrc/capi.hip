@@ -653,6 +653,13 @@ int fdi4_decode_step(const void* query, int query_dtype, int batch, int num_q_he
   if (!fused) {
     // Two launches: the append writes the advanced lengths to lens_next, the
     // decode attends over them and copies them back to the cache's lengths.
+    // Everything the decode checks is checked before the append writes the
+    // cache, so a rejected call leaves the cache as it was. The decode's plan
+    // (and so its split count and workspace) depends on the shapes only.
+    if (a.num_splits > 1 &&
+        (!workspace || !aligned(workspace, kAlign) ||
+         workspace_bytes < decode_ws_bytes(batch, num_q_heads, cache->head_dim, a.num_splits)))
+      return hipErrorInvalidValue;
     ap.lens_next = lens_next;
     hipError_t e = fdi4::launch_append_paged(ap, cache->head_dim, group_rows, batch,
                                              cache->num_kv_heads, stream);
@@ -964,6 +971,20 @@ int fdi4_fake_quantize(const void* k, int key_dtype, int batch, int heads, int s
   a.scale_recip = scale_op == FDI4_SCALE_RECIPROCAL ? 1 : 0;
   a.nsplit = a.cw = a.vpr = a.rpp = 0;
   return fdi4::launch_fake_quant(a, key_dtype, rounding, batch, heads, stream);
+}
+
+int fdi4_dequantize_int4(const uint8_t* q, int64_t rows, int num_channels, int64_t q_row_stride,
+                         int packed, const float* scale, const float* zp,
+                         int64_t s_row_stride, int64_t s_channel_stride, float* out,
+                         int64_t out_row_stride, hipStream_t stream) {
+  if (rows < 0 || num_channels <= 0 || s_row_stride < 0 || s_channel_stride < 0)
+    return hipErrorInvalidValue;
+  if (rows == 0) return hipSuccess;
+  if (!q || !scale || !zp || !out) return hipErrorInvalidValue;
+  const int64_t qcols = packed ? (num_channels + 1) / 2 : num_channels;
+  if (q_row_stride < qcols || out_row_stride < num_channels) return hipErrorInvalidValue;
+  return fdi4::launch_dequantize(q, rows, num_channels, q_row_stride, packed != 0, scale, zp,
+                                 s_row_stride, s_channel_stride, out, out_row_stride, stream);
 }
 
 int fdi4_pack_int4(const uint8_t* q, int64_t rows, int num_channels, int64_t q_row_stride,

@@ -79,14 +79,14 @@ __device__ __forceinline__ void step_append(const DecodeArgs& a, int b, int hk, 
 // start); the last to arrive writes the new length and clears the counter for
 // the next step. A relaxed device-scope atomic: the count is all the
 // arrivals need to agree on.
-__device__ __forceinline__ void step_arrive(const DecodeArgs& a, int b, int T) {
+__device__ __forceinline__ void step_arrive(const DecodeArgs& a, int b, int len_after) {
   if (threadIdx.x != 0) return;
   const int n = gridDim.x * gridDim.y;
   const int prev =
       __hip_atomic_fetch_add(a.step.arrive + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (prev == n - 1) {
     __hip_atomic_store(a.step.arrive + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    a.step.lens[b] = T;
+    a.step.lens[b] = len_after;
   }
 }
 
@@ -138,14 +138,19 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   __shared__ int open_done;
 
   const int cpp = (a.page_rows + 15) >> 4;
-  // With STEP, token t_app = seq_lens[b] is appended (none when the sequence
-  // already fills the cache) and the decode attends over t_app + 1 rows.
-  int T, t_app = -1;
+  // With STEP, token t_app = seq_lens[b] is appended when 0 <= t_app < cap
+  // and the decode attends over t_app + 1 rows, the length advancing to
+  // t_app + 1. A length outside [0, cap) appends nothing, is left as read,
+  // and the decode attends over it clamped to [0, cap] -- what the append
+  // kernel and the two-launch step do with such a length.
+  int T, t_app = -1, len_after = 0;
   if constexpr (STEP) {
     const int cap = a.max_pages * a.page_rows;
-    const int t = min(max(ld_ro(a.seq_lens, b), 0), cap);
-    t_app = t < cap ? t : -1;
-    T = t_app >= 0 ? t + 1 : t;
+    const int raw = ld_ro(a.seq_lens, b);
+    const bool fits = raw >= 0 && raw < cap;
+    t_app = fits ? raw : -1;
+    T = fits ? raw + 1 : min(max(raw, 0), cap);
+    len_after = fits ? raw + 1 : raw;
   } else {
     T = seq_len_of(a, b);
   }
@@ -462,7 +467,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     a.ws_ml[2 * pi + 1] = (double)l;
   }
   hand_back_length(a, b);
-  if constexpr (STEP) step_arrive(a, b, T);
+  if constexpr (STEP) step_arrive(a, b, len_after);
 }
 
 // Log-sum-exp merge of the split partials: grid (Hq, B), one thread per

@@ -127,6 +127,10 @@ hipError_t launch_append_paged(const AppendArgs& a, int D, int group, int batch,
 hipError_t launch_pack(const uint8_t* q, int64_t rows, int C, int64_t q_stride, uint8_t* out,
                        int64_t o_stride, int out_cols, hipStream_t st);
 
+hipError_t launch_dequantize(const uint8_t* q, int64_t rows, int C, int64_t q_stride, int packed,
+                             const float* scale, const float* zp, int64_t s_rs, int64_t s_cs,
+                             float* out, int64_t o_stride, hipStream_t st);
+
 hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hipStream_t st);
 
 hipError_t launch_decode_gqa(const DecodeArgs& a, int D, int v_dtype, int batch, int hg,

@@ -835,4 +835,47 @@ hipError_t launch_pack(const uint8_t* q, int64_t rows, int C, int64_t q_stride, 
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Dequantization of stored INT4 values (reference dequantize_int4_ref,
+// src/quantize_int4_ref.py:87-136): out[r, c] = q*s - zp*s with
+// s = scale[r*s_rs + c*s_cs], zp likewise -- two float32 products, each
+// rounded, then a rounded subtraction, as NumPy evaluates the formula. q is
+// one value per byte (its full byte value, as the reference's astype) or two
+// nibbles per byte (packed, channel c in the low nibble of byte c/2 when c is
+// even, the high nibble when odd). One thread per output element.
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ q, int64_t rows,
+                                                      int C, int64_t q_stride, int packed,
+                                                      const float* __restrict__ scale,
+                                                      const float* __restrict__ zp, int64_t s_rs,
+                                                      int64_t s_cs, float* __restrict__ out,
+                                                      int64_t o_stride) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * C) return;
+  const int64_t r = idx / C;
+  const int c = (int)(idx - r * C);
+  unsigned v;
+  if (packed) {
+    v = (q[r * q_stride + (c >> 1)] >> (4 * (c & 1))) & 15u;
+  } else {
+    v = q[r * q_stride + c];
+  }
+  const int64_t si = r * s_rs + (int64_t)c * s_cs;
+  const float sc = scale[si];
+  out[r * o_stride + c] = __fsub_rn(__fmul_rn((float)v, sc), __fmul_rn(zp[si], sc));
+}
+
+hipError_t launch_dequantize(const uint8_t* q, int64_t rows, int C, int64_t q_stride, int packed,
+                             const float* scale, const float* zp, int64_t s_rs, int64_t s_cs,
+                             float* out, int64_t o_stride, hipStream_t st) {
+  const int64_t total = rows * C;
+  if (total == 0) return hipSuccess;
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, st, q, rows, C,
+                     q_stride, packed, scale, zp, s_rs, s_cs, out, o_stride);
+  return hipGetLastError();
+}
+
 }  // namespace fdi4

@@ -105,6 +105,8 @@ SIGNATURES = {
                                           c_int64, c_int, c_void_p]),
     "fdi4_merge_splits": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
                                   c_int64, c_int64, c_void_p]),
+    "fdi4_dequantize_int4": (c_int, [c_void_p, c_int64, c_int, c_int64, c_int, c_void_p,
+                                     c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p]),
     "fdi4_pack_int4": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_int64, c_int,
                                c_void_p]),
     "fdi4_fake_quantize": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int64,

@@ -168,6 +168,72 @@ def pack_int4_device(q, out_cols: int = 0):
     return load_binding().pack_int4(q, out_cols)
 
 
+def dequantize_int4(q, scale, zp, target_shape: Optional[Tuple] = None,
+                    per_channel: bool = True, packed: bool = False,
+                    num_channels: Optional[int] = None):
+    """INT4 values back to float32 on the GPU: ``q*scale - zp*scale``, two
+    rounded float32 products and a rounded subtraction, bit-exact with the
+    reference's dequantize_int4_ref (src/quantize_int4_ref.py:87-136).
+
+    Args:
+        q: quantized values, one per byte (uint8, or any integer type with
+           values in [0, 255]); with ``packed=True`` nibble pairs along the
+           last axis (``pack_int4``), ``num_channels`` values per row
+           (default: twice the bytes).
+        scale, zp: per_channel -- the last axis's scales, broadcast over the
+           leading axes (fewer dims are prepended, as in the reference);
+           per-row -- the leading axes' scales, broadcast over the last axis
+           (dims are appended). Any shape that then broadcasts to the output.
+        target_shape: reshape the result to it.
+
+    NumPy inputs give a NumPy result; torch tensors give a float32 tensor on
+    the GPU.
+    """
+    _require_device(None)
+    is_tensor = isinstance(q, torch.Tensor)
+    dev = torch.device("cuda") if not is_tensor or not q.is_cuda else q.device
+    qt = q if is_tensor else torch.from_numpy(np.ascontiguousarray(q))
+    if qt.dim() < 1:
+        raise ValueError("q must have at least one axis")
+    if qt.dtype != torch.uint8:
+        if qt.is_floating_point() or qt.is_complex() or qt.dtype == torch.bool:
+            raise TypeError(f"q must hold integers, got {qt.dtype}")
+        if qt.numel() and (int(qt.min()) < 0 or int(qt.max()) > 255):
+            raise ValueError("q values must lie in [0, 255]")
+        qt = qt.to(torch.uint8)
+    qt = qt.to(dev)
+    nbytes = qt.shape[-1]
+    C = (num_channels if num_channels is not None else 2 * nbytes) if packed else nbytes
+    if packed and nbytes != (C + 1) // 2:
+        raise ValueError(f"{nbytes} packed bytes per row cannot hold {C} channels")
+    out_shape = tuple(qt.shape[:-1]) + (C,)
+    rows = int(np.prod(out_shape[:-1], dtype=np.int64))
+
+    def _as_tensor(a):
+        t = a if isinstance(a, torch.Tensor) else torch.from_numpy(np.asarray(a))
+        t = t.to(device=dev, dtype=torch.float32)
+        while t.dim() < len(out_shape):
+            t = t.unsqueeze(0) if per_channel else t.unsqueeze(-1)
+        try:
+            return torch.broadcast_to(t, out_shape).reshape(rows, C)
+        except RuntimeError as exc:
+            raise ValueError(f"scale/zp of shape {tuple(a.shape)} do not broadcast to "
+                             f"{out_shape}") from exc
+
+    s2, z2 = _as_tensor(scale), _as_tensor(zp)
+    if s2.stride() != z2.stride() or min(s2.stride()) < 0:
+        s2, z2 = s2.contiguous(), z2.contiguous()
+    q2 = qt.reshape(rows, nbytes)
+    if q2.stride(1) != 1:
+        q2 = q2.contiguous()
+    out = load_binding().dequantize_int4(q2, s2, z2, int(C), bool(packed)).reshape(out_shape)
+    if target_shape is not None:
+        out = out.reshape(target_shape)
+    if is_tensor:
+        return out
+    return out.cpu().numpy()
+
+
 # ---------------------------------------------------------------------------
 # attention over a list of pages (the reference's shared page stream)
 # ---------------------------------------------------------------------------

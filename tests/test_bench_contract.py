@@ -36,3 +36,17 @@ def test_no_visible_device_fails_loudly():
     assert r.returncode == 1
     assert "unavailable" in r.stderr
     assert r.stdout.strip() == ""
+
+
+def test_headline_window_is_steady_state_whatever_the_steps():
+    """The roofline figure is timed over at least 400 back-to-back launches in
+    20 blocks (the median over blocks then has 20 samples) for any --steps,
+    including the driver's short runs."""
+    sys.path.insert(0, ROOT)
+    import bench
+    for steps in (1, 5, 20, 200, 400):
+        blocks, per = bench.window_shape(steps)
+        assert blocks == 20 and blocks * per >= 400
+    blocks, per = bench.window_shape(1000)
+    assert blocks == 20 and blocks * per >= 1000
+    assert bench.median([3.0, 1.0, 2.0]) == 2.0 and bench.median([4.0, 1.0, 2.0, 3.0]) == 2.5

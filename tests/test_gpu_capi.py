@@ -231,3 +231,63 @@ def test_advance_pair_through_ctypes():
         capi.K_F32, ref.stride(0), ref.stride(1), 1, None, 0, _stream()), "decode_paged_ex")
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+def test_decode_step_rejects_a_bad_workspace_before_touching_the_cache():
+    """fdi4_decode_step on its two-launch path (grouped query heads, several
+    splits) with no workspace, a short one and a misaligned one: each call
+    returns hipErrorInvalidValue and leaves pages, values, scales, staging
+    rows, lengths and lens_next bitwise as they were; with the workspace the
+    library asks for, the same call appends and advances."""
+    import torch
+    from flash_decode_int4 import capi
+    from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
+    lib = capi.load()
+    B, H, HQ, D = 2, 4, 16, 128
+    c = INT4PagedSequenceCache(num_pages=2 * 128 + 8, num_kv_heads=H, head_dim=D, max_seqs=B,
+                               max_seq_len=2048)
+    g = torch.Generator(device="cuda").manual_seed(33)
+    k = torch.randn(B, H, 1500, D, device="cuda", generator=g)
+    c.prefill(k, torch.randn_like(k), [1500, 700])
+    c.reserve(B, 1)
+    kn = torch.randn(B, H, D, device="cuda", generator=g)
+    vn = torch.randn(B, H, D, device="cuda", generator=g)
+    q = torch.randn(B, HQ, D, device="cuda", generator=g)
+    out = torch.zeros(B, HQ, D, device="cuda")
+    kp, v, s = c.k_pages, c.v_pages, c.k_scale
+    desc = capi.PagedCache(
+        k_pages=kp.data_ptr(), k_page_stride=kp.stride(0), k_head_stride=kp.stride(1),
+        k_row_stride=kp.stride(2), v_pages=v.data_ptr(), v_dtype=capi.V_F32,
+        v_page_stride=v.stride(0), v_head_stride=v.stride(1), v_row_stride=v.stride(2),
+        k_scale=s.data_ptr(), k_zp=c.k_zp.data_ptr(), s_batch_stride=s.stride(0),
+        s_head_stride=s.stride(1), s_group_stride=s.stride(2), s_page_stride=0,
+        page_table=c.page_table.data_ptr(), pt_batch_stride=c.page_table.stride(0),
+        seq_lens=c.seq_lens.data_ptr(), page_lens=None, pl_batch_stride=0, num_kv_heads=H,
+        head_dim=D, page_rows=16, pages_per_group=8, max_pages=c.page_table.shape[1],
+        num_pages=kp.shape[0])
+    splits = lib.fdi4_decode_num_splits(B, HQ, desc)
+    assert splits > 1
+    need = lib.fdi4_decode_workspace_bytes(B, HQ, D, splits)
+    ws = torch.empty(need + 256, dtype=torch.uint8, device="cuda")
+    st = c.k_stage
+    nxt, cnt = c._lens_next, c._step_counters
+
+    def call(ptr, nbytes):
+        return lib.fdi4_decode_step(
+            _ptr(q), capi.K_F32, B, HQ, q.stride(0), q.stride(1), _ptr(kn), kn.stride(0),
+            kn.stride(1), _ptr(vn), vn.stride(0), vn.stride(1), _ptr(st), st.stride(0),
+            st.stride(1), st.stride(2), 128, desc, _ptr(out), capi.K_F32, out.stride(0),
+            out.stride(1), _ptr(cnt), _ptr(nxt), ptr, nbytes, _stream())
+
+    names = ("k_pages", "v_pages", "k_scale", "k_zp", "k_stage", "seq_lens", "_lens_next")
+    before = {n: getattr(c, n).clone() for n in names}
+    for ptr, nbytes in ((None, 0), (_ptr(ws), need - 256),
+                        (ctypes.c_void_p(ws.data_ptr() + 4), need)):
+        assert call(ptr, nbytes) == 1          # hipErrorInvalidValue
+        torch.cuda.synchronize()
+        for n in names:
+            assert torch.equal(getattr(c, n), before[n]), n
+    capi.check(call(_ptr(ws), need), "decode_step")
+    torch.cuda.synchronize()
+    assert c.seq_lens[:B].tolist() == [1501, 701]
+    assert torch.isfinite(out).all()

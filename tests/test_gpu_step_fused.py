@@ -181,3 +181,57 @@ def test_fused_step_at_the_anchor_size():
         assert torch.equal(out_new, out_old), i
     _same(new, old, "anchor")
     assert int(new._step_counters.abs().sum()) == 0
+
+
+def _reference_step(c, kn, vn, q, after, splits):
+    """Append kernel (which skips a position outside [0, capacity)), the
+    lengths set to `after`, decode with `splits` splits."""
+    import torch
+    from flash_decode_int4._lib import load_binding
+    B = kn.shape[0]
+    load_binding().append_paged(kn, vn, c.k_stage[:B], c.k_pages, c.v_pages, c.k_scale[:B],
+                                c.k_zp[:B], c.page_table[:B], c.seq_lens[:B], c.group_rows)
+    c.seq_lens[:B] = torch.tensor(after, dtype=torch.int32, device="cuda")
+    return c.decode(q, num_splits=splits)
+
+
+@pytest.mark.parametrize("form", ["one_launch", "two_launch"])
+def test_step_lengths_outside_the_cache(form):
+    """Lengths below 0 and above the cache's capacity: no token is appended,
+    the length is left as read, and the decode attends over it clamped to
+    [0, capacity] -- in the one-launch step, in the two-launch step, and in
+    the append kernel + decode form, bit for bit (outputs, pages, scales,
+    values, staging rows, lengths)."""
+    import torch
+    from flash_decode_int4 import capi
+    from flash_decode_int4._lib import load_binding
+    B, H, D = 5, 2, 128
+    lens0 = [100, 40, 200, 17, 511]
+    (new, old), g = _twins(B, H, D, lens0, 16, 128, "float32", 512, 71)
+    cap = new.max_pages_per_seq * new.page_rows
+    assert cap == 512
+    raw = [-5, 40, 2 ** 31 - 1, cap + 9, 511]
+    after = [-5, 41, 2 ** 31 - 1, cap + 9, 512]
+    for c in (new, old):
+        c.seq_lens[:B] = torch.tensor(raw, dtype=torch.int32, device="cuda")
+    kn = torch.randn(B, H, D, device="cuda", generator=g)
+    vn = torch.randn(B, H, D, device="cuda", generator=g)
+    q = torch.randn(B, H, D, device="cuda", generator=g)
+    # One split takes the one-launch step; four-wave workgroups and a high
+    # wave target give two splits (32 chunks of 4 per wave), so the
+    # two-launch step.
+    tune = {"decode_waves": 4,
+            "decode_target_waves": 1 if form == "one_launch" else 4096}
+    C = load_binding()
+    with capi.tuning(**tune):
+        splits = int(C.decode_num_splits(B, H, H, D, new.max_pages_per_seq, 16))
+        assert (splits == 1) == (form == "one_launch")
+        out_new = load_step(new, kn, vn, q)
+        out_old = _reference_step(old, kn, vn, q, after, splits)
+    torch.cuda.synchronize()
+    assert new.seq_lens[:B].tolist() == after
+    assert torch.isfinite(out_new).all()
+    assert torch.equal(out_new[0], torch.zeros_like(out_new[0]))    # length -5: no rows
+    assert torch.equal(out_new, out_old)
+    _same(new, old, form)
+    assert int(new._step_counters.abs().sum()) == 0

@@ -127,6 +127,42 @@ class TestBackendHonesty:
         assert st["has_extension"] is True
 
 
+class TestPackageExports:
+    """The reference package's public names (src/__init__.py:20-56): its
+    availability flags, here False because this package ships neither the
+    NumPy reference functions nor a Pallas backend, and a device
+    dequantize_int4 in place of dequantize_int4_ref."""
+
+    def test_reference_flags_are_present_and_honest(self):
+        import flash_decode_int4 as pkg
+        assert pkg.HAS_QUANT_REF is False
+        assert pkg.HAS_DECODE_REF is False
+        assert pkg.HAS_PALLAS is False
+        assert isinstance(pkg.HAS_CUDA, bool)
+        for name in ("HAS_QUANT_REF", "HAS_DECODE_REF", "HAS_PALLAS", "HAS_CUDA",
+                     "dequantize_int4", "pack_int4", "unpack_int4", "packed_nbytes"):
+            assert name in pkg.__all__, name
+
+    def test_oracle_functions_are_not_reexported(self):
+        import flash_decode_int4 as pkg
+        for name in ("quantize_int4_ref", "dequantize_int4_ref", "flash_decode_ref",
+                     "online_softmax_ref"):
+            assert not hasattr(pkg, name), name
+
+    def test_backend_info_reports_the_flags(self, capsys):
+        import flash_decode_int4 as pkg
+        pkg.backend_info()
+        out = capsys.readouterr().out
+        assert "Quantization reference" in out and "Pallas" in out
+
+    @pytest.mark.skipif(ops.HAS_HIP, reason="checks the no-GPU failure mode")
+    def test_dequantize_without_gpu_fails_loudly(self):
+        import flash_decode_int4 as pkg
+        with pytest.raises(RuntimeError):
+            pkg.dequantize_int4(np.zeros((2, 4), np.uint8), np.ones(4, np.float32),
+                                np.zeros(4, np.float32))
+
+
 class TestHostPacking:
 
     @pytest.mark.parametrize("shape", [(256, 64), (10, 7), (4, 128, 32), (3, 1), (1, 2)])
@@ -414,6 +450,17 @@ def check_invalid_arguments_are_rejected():
     assert lib.fdi4_decode_workspace_bytes(64, 64, 256, 2) > capi.NOALLOC_SCRATCH_BYTES
     assert lib.fdi4_decode_paged_noalloc(q, 64, 64, 1 << 14, 256, ctypes.byref(wide), q,
                                          1 << 14, 256, 2, None) == bad
+    # Dequantization: missing pointers, rows shorter than the channels they
+    # hold (unpacked and packed), negative scale strides.
+    assert lib.fdi4_dequantize_int4(None, 4, 8, 8, 0, q, q, 0, 1, q, 8, None) == bad
+    assert lib.fdi4_dequantize_int4(q, 4, 8, 8, 0, q, None, 0, 1, q, 8, None) == bad
+    assert lib.fdi4_dequantize_int4(q, 4, 8, 7, 0, q, q, 0, 1, q, 8, None) == bad
+    assert lib.fdi4_dequantize_int4(q, 4, 9, 4, 1, q, q, 0, 1, q, 9, None) == bad
+    assert lib.fdi4_dequantize_int4(q, 4, 8, 8, 0, q, q, 0, 1, q, 7, None) == bad
+    assert lib.fdi4_dequantize_int4(q, 4, 8, 8, 0, q, q, -1, 1, q, 8, None) == bad
+    assert lib.fdi4_dequantize_int4(q, 4, 0, 8, 0, q, q, 0, 1, q, 8, None) == bad
+    # Zero rows: nothing to do, no device call.
+    assert lib.fdi4_dequantize_int4(None, 0, 8, 8, 0, None, None, 0, 1, None, 8, None) == 0
 
 
 def check_typed_decode_rejects_unknown_element_types():

@@ -106,3 +106,45 @@ def test_noalloc_single_split_needs_no_scratch():
                                      0, _stream()))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out_na.cpu().numpy(), out_ws.cpu().numpy())
+
+
+def test_noalloc_replayed_from_a_graph():
+    """After one eager call on the device (the first call looks the array's
+    address up, which is not a stream operation), the call is captured in a
+    HIP graph; each replay, with new queries written between replays, equals
+    the workspace call on the same queries bit for bit."""
+    import torch
+    from flash_decode_int4 import capi
+    lib = capi.load()
+    cache, keep = _cache(4, [1200, 333, 0], seed=31)
+    B, hq, D, splits = 3, 16, 128, 4
+    rng = np.random.RandomState(32)
+    q = torch.from_numpy(rng.randn(B, hq, D).astype(np.float32)).cuda()
+    out_g = torch.full((B, hq, D), float("nan"), device="cuda")
+    nbytes = lib.fdi4_decode_workspace_bytes(B, hq, D, splits)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    ref = torch.empty(B, hq, D, device="cuda")
+
+    def noalloc():
+        return lib.fdi4_decode_paged_noalloc(_ptr(q), B, hq, q.stride(0), q.stride(1), cache,
+                                             _ptr(out_g), out_g.stride(0), out_g.stride(1),
+                                             splits, _stream())
+
+    capi.check(noalloc(), "decode_paged_noalloc (eager)")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = noalloc()
+    assert rc == 0
+    for r in range(3):
+        q.copy_(torch.from_numpy(rng.randn(B, hq, D).astype(np.float32)))
+        out_g.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        capi.check(lib.fdi4_decode_paged(_ptr(q), B, hq, q.stride(0), q.stride(1), cache,
+                                         _ptr(ref), ref.stride(0), ref.stride(1), splits,
+                                         _ptr(ws), nbytes, _stream()), "decode_paged")
+        torch.cuda.synchronize()
+        assert torch.isfinite(out_g).all(), r
+        assert torch.equal(out_g, ref), r
