@@ -26,7 +26,9 @@
 //      changes; the scale/zero-point block of the next group is prefetched
 //      with one 16-byte load per lane and staged through LDS.
 //   softmax: wave-wide fp64 max over the chunk (DPP / ds_swizzle / permlane
-//      swaps), float32 exp of the fp64 differences.
+//      swaps), the hardware 2^x of the fp64 differences times log2(e)
+//      (exp2_of; also in the LDS merge of the waves' partials and in the
+//      split merge).
 //   V: fully coalesced 16-byte loads (VPR lanes per row); the probabilities
 //      go through a 16-entry LDS row per wave; float32 FMA accumulation.
 //   The K and V loads of the next chunk are issued before the current chunk
@@ -97,7 +99,7 @@ __device__ __forceinline__ void step_arrive(const DecodeArgs& a, int b, int len_
 __device__ __forceinline__ void merge_term(double m, double ms, float acc, double lraw, float& o,
                                            float& l) {
   if (m == -INFINITY) return;
-  const float e = expf((float)(m - ms));
+  const float e = exp2_of(m - ms);
   o = __builtin_fmaf(e, acc, o);
   l = __builtin_fmaf(e, (float)lraw, l);
 }
@@ -341,12 +343,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     for (int i = 1; i < G::KLD; ++i) mc = fmax(mc, lg[i]);
     mc = allreduce_max<G::LPT, 64>(mc);
     const double m_new = fmax(m_run, mc);
-    const float corr = expf((float)(m_run - m_new));
+    const float corr = exp2_of(m_run - m_new);
     m_run = m_new;
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < G::KLD; ++i) {
-      const float p = expf((float)(lg[i] - m_new));
+      const float p = exp2_of(lg[i] - m_new);
       if (kq == 0) p_s[w][i * G::TPW + ktok] = p;
       psum += p;
     }
@@ -447,7 +449,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   float l = 0.f;
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
-    ew[i] = (m_s[i] == -INFINITY) ? 0.f : expf((float)(m_s[i] - ms));
+    ew[i] = (m_s[i] == -INFINITY) ? 0.f : exp2_of(m_s[i] - ms);
     l = __builtin_fmaf(ew[i], l_s[i], l);
   }
   const int64_t pi = ((int64_t)b * a.num_q_heads + h) * a.num_splits + split;

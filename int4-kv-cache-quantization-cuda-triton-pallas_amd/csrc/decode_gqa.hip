@@ -333,7 +333,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gqa_kernel(DecodeArgs a) {
     float o = 0.f, l = 0.f;
 #pragma unroll
     for (int i = 0; i < WAVES; ++i) {
-      const float e = (m_s[i][h] == -INFINITY) ? 0.f : expf((float)(m_s[i][h] - ms));
+      const float e = (m_s[i][h] == -INFINITY) ? 0.f : exp2_of(m_s[i][h] - ms);
       l = __builtin_fmaf(e, l_s[i][h], l);
       o = __builtin_fmaf(e, acc_s[i][h][d], o);
     }
