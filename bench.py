@@ -72,7 +72,7 @@ Prints ONE JSON line on stdout (progress lines go to stderr). Options:
 --workload (anchor, sweep_512 ... llama, ragged), --tokens (every sequence at
 that length), --splits, --value-dtype float16|bfloat16, --no-cpu, --no-pmc,
 --no-trace (both required when this script itself runs under rocprofv3),
---decode-only (the decode timing alone).
+--decode-only (the workload's decode and quantizer timings alone).
 """
 
 import argparse
@@ -116,9 +116,8 @@ def parse():
     p.add_argument("--no-pmc", action="store_true",
                    help="skip the rocprofv3 --pmc traffic runs (required under rocprofv3)")
     p.add_argument("--decode-only", action="store_true",
-                   help="time the decode of the workload and nothing else (no other paths, "
-                        "PMC or CPU legs): the command a rocprofv3 kernel trace of the "
-                        "headline loop runs")
+                   help="time the decode and the grouped quantizer of the workload and "
+                        "nothing else (no other paths, trace, PMC or CPU legs)")
     p.add_argument("--step-only", action="store_true",
                    help="time the serving step (B8 H32 D128 around 2048 tokens, eager steps "
                         "and the plain decode of the same cache) and nothing else, then run "
@@ -224,7 +223,7 @@ def time_reference_config(steps, warmup):
                     "NVIDIA H100 (its README and results JSON); other hardware, context only"}
 
 
-def time_reference_quantizer(steps, warmup):
+def time_reference_quantizer(steps, warmup, window=True):
     """The reference's own quantizer benchmark semantics through the drop-in
     API: ops.quantize_int4 of one [rows, 128] float32 array, one scale group
     over all rows, one unpacked INT4 value per output byte (reference
@@ -250,12 +249,24 @@ def time_reference_quantizer(steps, warmup):
         host[f"rows_{rows}x{C}"] = (sets[0].cpu().numpy(), calls[0]())
         for i in range(warmup):
             calls[i % n_sets].run()
+        if not window:
+            # A counter pass: K calls over the rotated inputs.
+            for i in range(steps):
+                calls[i % n_sets].run()
+            torch.cuda.synchronize()
+            del sets, calls
+            torch.cuda.empty_cache()
+            continue
         nb, blk = window_shape(steps)
         us, us_med, _ = window_us(lambda i: calls[i % n_sets].run(), nb, blk)
+        # The same call on one input over and over (every read served by the
+        # caches): against the rotated figure, what reading the input from
+        # HBM costs the call.
+        res_us, _, _ = window_us(lambda i: calls[0].run(), nb, blk)
         nbytes = in_bytes + rows * C + 2 * C * 4
         out[f"rows_{rows}x{C}"] = {
             "us": round(us, 3), "us_median": round(us_med, 3), "bytes": nbytes,
-            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "resident_us": round(res_us, 3),
             "input_sets": n_sets, "reference_cuda_h100_us": ref_us}
         del sets, calls
         torch.cuda.empty_cache()
@@ -403,7 +414,7 @@ def interleaved_us(fa, fb, rounds=10, block=20):
     return median(ta), median(tb)
 
 
-def time_decode(sets, splits, steps, warmup):
+def time_decode(sets, splits, steps, warmup, window=True):
     import torch
     S, step, decode_only = decode_launchers(sets, splits)
 
@@ -424,6 +435,12 @@ def time_decode(sets, splits, steps, warmup):
     for i in range(warmup):
         step(i)
     out, wall, step_us = timed(step, steps)
+    if not window:
+        # A check or a counter pass: the K steps only.
+        return dict(splits=S, wall_s=wall, step_us=step_us, window_us=step_us,
+                    step_median_us=step_us, window_launches=steps, window_blocks=1,
+                    decode_us=step_us, decode_median_us=step_us, merge_us=0.0, last_out=out,
+                    last_set=(steps - 1) % len(sets))
     nb, blk = window_shape(steps)
     win_us, win_median, win_n = window_us(step, nb, blk, start=steps)
     if S == 1:
@@ -439,9 +456,10 @@ def time_decode(sets, splits, steps, warmup):
                 last_set=(steps - 1) % len(sets))
 
 
-def time_quantizer(sets, steps, warmup):
+def time_quantizer(sets, steps, warmup, window=True):
     """Grouped quantizer over the rotated input sets: (mean per launch over a
-    steady-state window, median over the window's blocks)."""
+    steady-state window, median over the window's blocks); window=False: K
+    launches (a counter pass)."""
     from flash_decode_int4 import ops
     g = sets[0]["w"]["group_rows"]
 
@@ -451,6 +469,10 @@ def time_quantizer(sets, steps, warmup):
 
     for i in range(warmup):
         q(i)
+    if not window:
+        for i in range(steps):
+            q(i)
+        return None, None
     nb, blk = window_shape(steps)
     mean, med, _ = window_us(q, nb, blk)
     return mean, med
@@ -845,13 +867,13 @@ def pmc_child(args):
     import torch
     sets, _ = build_sets(args.workload, args.value_dtype, n_sets_hint=1,
                          seq_lens=workload_lens(args))
-    r = time_decode(sets, args.splits, steps=3, warmup=1)
-    time_quantizer(sets, steps=3, warmup=1)
+    r = time_decode(sets, args.splits, steps=3, warmup=1, window=False)
+    time_quantizer(sets, steps=3, warmup=1, window=False)
     del sets
     torch.cuda.empty_cache()
     calibration_kernels()
     time_fake_quant(steps=2, warmup=1)
-    time_reference_quantizer(steps=3, warmup=1)
+    time_reference_quantizer(steps=3, warmup=1, window=False)
     print(json.dumps({"splits": r["splits"]}))
 
 
@@ -1069,7 +1091,7 @@ def main():
     st0 = sets[0]
     ref1 = ops.flash_decode_paged(st0["q"], st0["kp"], st0["v"], st0["s"], st0["z"], st0["pt"],
                                   st0["sl"], num_splits=1)
-    r = time_decode([st0], args.splits, steps=1, warmup=0)
+    r = time_decode([st0], args.splits, steps=1, warmup=0, window=False)
     gate = float((r["last_out"] - ref1).abs().max())
     if not (math.isfinite(gate) and gate < 2e-6 and bool(torch.isfinite(ref1).all())):
         print(f"bench.py: correctness gate failed (split vs single-split diff {gate})",
@@ -1139,6 +1161,9 @@ def main():
         "kernel_us_median": round(res["decode_median_us"], 3),
     }
     if args.decode_only:
+        qt, qt_median = time_quantizer(sets, args.steps, args.warmup)
+        line.update({"quantizer_us": round(qt, 3), "quantizer_us_median": round(qt_median, 3),
+                     "quantizer_hbm_frac": round(qbytes / (qt * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         line["roofline"] = roofline
         print(json.dumps(line), flush=True)
         return

@@ -23,9 +23,15 @@ split counts agree.
 """
 
 import json
+import warnings
 
 import numpy as np
 import pytest
+
+
+class ParityReport(UserWarning):
+    """Carries each workload's parity maxima into pytest's warnings summary,
+    which a quiet run (-q, output captured) still prints at its end."""
 
 from oracle.pool import paged_oracle_all
 
@@ -92,6 +98,11 @@ def _check_every_stream(label, st):
                max_hip_vs_f64=float(e64.max()), max_o32_vs_f64=float(eo.max()),
                oracle_workers=res["workers"], oracle_seconds=round(res["seconds"], 2))
     print("\n[parity] " + json.dumps(rec), flush=True)
+    warnings.warn(ParityReport(
+        f"[parity] {label}: {rec['streams']} streams, oracle-limited {rec['oracle_limited']}, "
+        f"key mismatches {rec['key_mismatch_streams']}, max|HIP-o32| strict "
+        f"{rec['max_hip_vs_o32_strict_streams']:.2e} all {rec['max_hip_vs_o32']:.2e}, "
+        f"max|HIP-f64| {rec['max_hip_vs_f64']:.2e}, max|o32-f64| {rec['max_o32_vs_f64']:.2e}"))
     assert np.isfinite(got).all(), label
     assert (got[~live] == 0).all(), label                      # empty sequences: exact zeros
     assert res["key_mismatch"] == 0, rec
