@@ -18,8 +18,10 @@ Clocks. `value` and `ms_per_step` come from the wall clock around exactly K
 host launch cost included). `decode_us` and the roofline figure come from
 HIP events on the launch stream around a steady-state window of at least 400
 back-to-back launches (20 blocks, an event between blocks, no host
-synchronization inside the window, whatever --steps is); `decode_us_median`
-is the median over the window's blocks. `roofline.trace_*` are the decode
+synchronization inside the window, whatever --steps is), which follows ~30
+ms of untimed launches (a GPU that has been idle runs its first ~15 ms of
+launches 1-7 % slower); `decode_us_median` is the median over the window's
+blocks. `roofline.trace_*` are the decode
 kernel's per-dispatch durations over the same window, from a rocprofv3
 --kernel-trace child process (`--no-trace` skips it). The quantizers and the
 other decode paths are timed over windows of the same shape.
@@ -303,13 +305,38 @@ def window_shape(steps):
     return WINDOW_BLOCKS, -(-per // WINDOW_BLOCKS)
 
 
-def window_us(fn, blocks, block, start=0):
-    """Back-to-back launches in `blocks` blocks of `block`, one event on the
-    launch stream before the first block and after every block, one
-    synchronize at the end (the GPU never idles inside the window). Returns
-    (mean per launch over the window, median over the blocks of the
-    per-launch time of a block, launches)."""
+#: GPU time spent in untimed launches before a window: a GPU that has been
+#: idle runs its first ~15 ms of back-to-back launches 1-7 % slower (B8 H32
+#: T2048 decode, blocks of 20 launches: 50-54 us, then a steady 49.0-49.3).
+SETTLE_MS = 30.0
+
+
+def settle(fn, start=0):
+    """Untimed back-to-back launches for about SETTLE_MS of GPU time (ten to
+    measure the launch, then as many as the rest needs); returns the next
+    launch index."""
     import torch
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(10):
+        fn(start + i)
+    e1.record()
+    torch.cuda.synchronize()
+    per_ms = max(e0.elapsed_time(e1) / 10, 1e-3)
+    n = max(0, math.ceil((SETTLE_MS - 10 * per_ms) / per_ms))
+    for i in range(n):
+        fn(start + 10 + i)
+    return start + 10 + n
+
+
+def window_us(fn, blocks, block, start=0):
+    """After settle(), back-to-back launches in `blocks` blocks of `block`,
+    one event on the launch stream before the first block and after every
+    block, one synchronize at the end (the GPU never idles inside the
+    window). Returns (mean per launch over the window, median over the blocks
+    of the per-launch time of a block, launches)."""
+    import torch
+    start = settle(fn, start)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(blocks + 1)]
     torch.cuda.synchronize()
     ev[0].record()
@@ -395,11 +422,12 @@ def decode_launchers(sets, splits):
 
 def interleaved_us(fa, fb, rounds=10, block=20):
     """Per-launch time of two launch sequences measured in alternating blocks
-    (A, B, A, B, ...) of `block` back-to-back launches, one event between
-    blocks and one synchronize at the end, so both see the same clocks and
-    memory state and the GPU never idles between blocks; returns the two
-    medians over the rounds."""
+    (A, B, A, B, ...) of `block` back-to-back launches after settle(), one
+    event between blocks and one synchronize at the end, so both see the same
+    clocks and memory state and the GPU never idles between blocks; returns
+    the two medians over the rounds."""
     import torch
+    settle(fa)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * rounds + 1)]
     torch.cuda.synchronize()
     ev[0].record()
@@ -982,8 +1010,9 @@ def pmc_traffic(args):
 
 def trace_child(args):
     """The headline's decode window alone, for a rocprofv3 --kernel-trace
-    child: the same input sets, warmup, then the steady-state window of the
-    decode kernel (window_shape(--steps)); prints its own event figures."""
+    child: the same input sets, warmup, then (after settle()) the
+    steady-state window of the decode kernel (window_shape(--steps)); prints
+    its own event figures."""
     sets, _ = build_sets(args.workload, args.value_dtype, seq_lens=workload_lens(args))
     S, step, decode_only = decode_launchers(sets, args.splits)
     fn = step if S == 1 else decode_only
@@ -1083,6 +1112,13 @@ def main():
     progress(f"building the {args.workload} input sets")
     sets, set_bytes = build_sets(args.workload, args.value_dtype, seq_lens=workload_lens(args))
     w0 = sets[0]["w"]
+    # The seq_len + 1 inputs are built now, so that the GPU does not sit idle
+    # between the headline window and the check timed right after it (an
+    # idle GPU starts the next launches at different clocks).
+    odd_sets = odd_bytes = None
+    if not args.decode_only:
+        odd_sets, odd_bytes = build_sets(args.workload, args.value_dtype,
+                                         seq_lens=w0["seq_lens"] + 1)
     vbytes = 4 if args.value_dtype == "float32" else 2
     qbytes = workloads.quantize_bytes(w0["seq_lens"], w0["heads"], w0["head_dim"])
 
@@ -1170,10 +1206,9 @@ def main():
     # No shape specialization (the reference bench re-runs at seq_len + 1): every
     # length + 1, so pages end one row into a fresh page and groups one row into
     # a fresh group; the output must be finite and the rate must hold. Timed
-    # right after the headline, then the two lengths in alternating blocks (the
-    # same clocks and memory state for both).
+    # right after the headline (inputs built before it), then the two lengths
+    # in alternating blocks (the same clocks and memory state for both).
     odd_lens = w0["seq_lens"] + 1
-    odd_sets, odd_bytes = build_sets(args.workload, args.value_dtype, seq_lens=odd_lens)
     progress("seq_len + 1 check")
     odd = time_decode(odd_sets, args.splits, max(args.steps // 2, 5), args.warmup)
     odd_ok = bool(torch.isfinite(odd["last_out"]).all())
