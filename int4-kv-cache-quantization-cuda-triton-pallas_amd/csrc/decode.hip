@@ -9,7 +9,8 @@
 //   grid (num_splits, Hq, B); a workgroup of WAVES wave64s owns one split,
 //   a contiguous range of 16-row chunks of one (sequence, q-head); each SIMD
 //   takes a quarter of the range, cut into ranges of its two waves (about
-//   18:14 between the SIMD's older and younger wave, the younger wave's last
+//   20:12 between the SIMD's older and younger wave with float32 values,
+//   18:14 with 16-bit values, the younger wave's last
 //   chunks a range of their own, see wave_segments); every range keeps its
 //   own (m, l, acc) and the ranges are merged through LDS in a fixed order.
 //   With one split the workgroup writes the output,
@@ -166,7 +167,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
   // The serving step's younger waves re-quantize first: the older waves take
   // the last range of each SIMD (the same partials, computed by other waves).
-  const WaveSegs ws = wave_segments(c_begin, c_end, w, WAVES, append);
+  const WaveSegs ws = wave_segments(c_begin, c_end, w, WAVES, append,
+                                    VDT == kVF32 ? kFirstShare32F32 : kFirstShare32);
   const int len1 = ws.p1 - ws.p0, len2 = ws.q1 - ws.q0, wlen = len1 + len2;
   // The wave's i-th chunk.
   auto cidx = [&](int i) { return i < len1 ? ws.p0 + i : ws.q0 + (i - len1); };

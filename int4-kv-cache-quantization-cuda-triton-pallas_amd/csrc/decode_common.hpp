@@ -149,11 +149,19 @@ __device__ __forceinline__ int pages_of(const DecodeArgs& a, int T) {
 // each), waves 0-3 finished their loops 6.5 us before waves 4-7 (38.6 against
 // 45.1 us), leaving one wave per SIMD, with half the loads in flight, for the
 // rest of the decode. The older wave therefore takes kFirstShare32 / 32 of
-// its SIMD's chunks (rounded to nearest) and the younger one the rest.
+// its SIMD's chunks (rounded to nearest) and the younger one the rest; the
+// per-head decode with float32 values gives it kFirstShare32F32 / 32 (in-process
+// A/B against 18/32, one box: B8 H32 T2048 -0.8 to -1.1 %, T1024 -2 %, T8192
+// -0.5 %, T512 and ragged B32 within 0.4 %; with 16-bit values 20/32 was
+// 1.5 % slower, 16/32 slower everywhere).
 #ifndef FDI4_FIRST_SHARE32
 #define FDI4_FIRST_SHARE32 18
 #endif
 constexpr int kFirstShare32 = FDI4_FIRST_SHARE32;
+#ifndef FDI4_FIRST_SHARE32_F32
+#define FDI4_FIRST_SHARE32_F32 20
+#endif
+constexpr int kFirstShare32F32 = FDI4_FIRST_SHARE32_F32;
 
 struct WaveRange {
   int c0, c1;      // the wave's chunks [c0, c1)
@@ -181,8 +189,8 @@ __device__ __forceinline__ WaveRange wave_chunks(int begin, int end, int w, int 
 // an online-softmax partial of its own (LDS slot s1, and s2 when s2 >= 0).
 // SIMD s = w % 4 takes the same consecutive chunks [S, E) as in wave_chunks
 // (n of them). With four waves that is the wave's one segment (slot w). With
-// eight, [S, E) is cut into three ranges: A = the first (n * kFirstShare32 +
-// 16) / 32 chunks, C = the last (n * kTailShare32 + 16) / 32 of the rest, B
+// eight, [S, E) is cut into three ranges: A = the first (n * first32 + 16) /
+// 32 chunks, C = the last (n * kTailShare32 + 16) / 32 of the rest, B
 // between; A's partial goes to slot s, B's to 4 + s, C's to 8 + s (12 slots,
 // merged in slot order). The older wave w < 4 takes A, the younger wave w + 4
 // takes B; C goes to the younger wave (then its segments B, C are contiguous)
@@ -202,7 +210,7 @@ struct WaveSegs {
 };
 
 __device__ __forceinline__ WaveSegs wave_segments(int begin, int end, int w, int waves,
-                                                  bool lend_tail) {
+                                                  bool lend_tail, int first32) {
   const int span = max(end - begin, 0);
   const int simds = min(waves, 4);
   const int s = w % simds;
@@ -215,7 +223,7 @@ __device__ __forceinline__ WaveSegs wave_segments(int begin, int end, int w, int
     r.p0 = S; r.p1 = E; r.q0 = r.q1 = E; r.s1 = w; r.s2 = -1;
     return r;
   }
-  const int first = (n * kFirstShare32 + 16) / 32;
+  const int first = (n * first32 + 16) / 32;
   const int tail = min((n * kTailShare32 + 16) / 32, n - first);
   const int a1 = S + first, c0 = E - tail;
   if (w < simds) {
