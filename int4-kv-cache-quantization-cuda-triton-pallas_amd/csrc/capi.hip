@@ -115,22 +115,47 @@ struct DecodePlan {
   int splits;
 };
 
+// The per-head decode with float32 values at D = 128 (512-byte value rows)
+// runs four waves, one per SIMD, and aims at one wave per SIMD
+// (kTargetWaves / 2) while the streams at four waves stay within kTargetWaves:
+// one wave streams a 16-row chunk of 8 KB of values with enough loads in
+// flight, and no SIMD is shared by an older and a younger wave that finish
+// apart. In-process A/B against eight waves and kTargetWaves, one box: B8 H32
+// T512 16.15 -> 15.61 us, T2048 48.8 -> 47.8, T8192 182.0 -> 181.4, B16 H32
+// T2048 94.7 -> 93.4, B1 H8 T1024 13.5 -> 10.7 (four splits against two);
+// slower with 256-byte rows (D=64: 27.8 -> 30.0 us; float16 values at D=128:
+// 31.3 -> 35.7) and with more streams (B32 H32, ragged lengths to 8192:
+// 321.5 -> 346.2 us; B64 H32 T4096: 713.2 -> 716.5). (At D = 256 the
+// four-wave kernel needs more than 256 registers, one wave per SIMD.)
+bool one_wave_per_simd(int d, int v_dtype, int64_t streams) {
+  return d == 128 && v_dtype == FDI4_V_F32 && streams * 4 <= kTargetWaves;
+}
+
 // Launch shape of a decode: heads per workgroup, waves per workgroup (the
 // grouped kernel at D=256 has registers for four), and the split count that
-// gives about kTargetWaves waves over the (sequence, head group) streams.
+// gives about kTargetWaves waves over the (sequence, head group) streams. The
+// fused serving step takes the same shape (and so gives the same bits as the
+// append and the decode); with four decode waves its kernel adds four helper
+// waves that re-quantize the open group meanwhile.
 DecodePlan plan_decode(int batch, int hq, int hq_per_kv, int d, int v_dtype, int chunks) {
   DecodePlan p;
   p.mfma = use_mfma(d) ? 1 : 0;
   p.heads_per_wg = p.mfma ? pick_heads_per_wg_mfma(d, v_dtype, hq_per_kv)
                           : pick_heads_per_wg(d, hq_per_kv);
   if (p.heads_per_wg == 1) p.mfma = 0;
-  p.waves = (!p.mfma && p.heads_per_wg > 1 && d == 256) ? 4 : pick_waves(chunks);
+  const int64_t streams = (int64_t)batch * (hq / p.heads_per_wg);
+  const bool per_simd = !p.mfma && p.heads_per_wg == 1 && one_wave_per_simd(d, v_dtype, streams);
+  const int forced = g_tuning[FDI4_TUNE_DECODE_WAVES].load(std::memory_order_relaxed);
+  if (!p.mfma && p.heads_per_wg > 1 && d == 256) p.waves = 4;
+  else if (per_simd && forced == 0) p.waves = 4;
+  else p.waves = pick_waves(chunks);
   if (chunks <= 0) {
     p.splits = 1;
     return p;
   }
   const int tw = g_tuning[FDI4_TUNE_DECODE_TARGET_WAVES].load(std::memory_order_relaxed);
-  const int64_t target = tw > 0 ? tw : kTargetWaves;
+  const int64_t target =
+      tw > 0 ? tw : (per_simd && p.waves == 4 ? kTargetWaves / 2 : kTargetWaves);
   const int64_t per_split = (int64_t)batch * (hq / p.heads_per_wg) * p.waves;
   const int s = (int)((target + per_split - 1) / per_split);
   const int smax = std::max(1, chunks / (p.waves * kMinChunksPerWave));

@@ -13,6 +13,8 @@
 //   18:14 with 16-bit values, the younger wave's last
 //   chunks a range of their own, see wave_segments); every range keeps its
 //   own (m, l, acc) and the ranges are merged through LDS in a fixed order.
+//   (The fused serving step with four decode waves adds four helper waves
+//   that re-quantize the open group and own no chunks.)
 //   With one split the workgroup writes the output,
 //   otherwise (m, l, acc[D]) goes to the workspace and merge_kernel combines
 //   the splits with a log-sum-exp weighting.
@@ -105,10 +107,21 @@ __device__ __forceinline__ void merge_term(double m, double ms, float acc, doubl
   l = __builtin_fmaf(e, (float)lraw, l);
 }
 
+// Waves of a decode workgroup that only re-quantize: the fused serving step
+// with four decode waves adds four, which re-quantize the open group while
+// the decode waves stream (with eight decode waves the younger four do it
+// first, then decode).
+template <int WAVES, bool STEP>
+constexpr int helper_waves() {
+  return STEP && WAVES == 4 ? 4 : 0;
+}
+
 template <int D, int VDT, int WAVES, bool STEP>
-__global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__((WAVES + helper_waves<WAVES, STEP>()) * 64) void decode_kernel(
+    DecodeArgs a) {
   using G = Geo<D, VDT>;
-  constexpr int NT = WAVES * 64;
+  constexpr int HW = helper_waves<WAVES, STEP>();
+  constexpr int NT = (WAVES + HW) * 64;
 
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int hk = h / a.hq_per_kv;
@@ -116,6 +129,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   // The wave index is uniform across the wave; saying so keeps the chunk loop
   // counters in scalar registers and the page-table reads on the scalar unit.
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool helper = w >= WAVES;     // a re-quantizing helper wave (no chunks)
   const int kq = lane % G::LPT;       // channel slice of this lane (K)
   const int ktok = lane / G::LPT;     // key row within a sweep
   const int vrow = lane / G::VPR;     // value row within a sweep
@@ -167,9 +181,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
   // The serving step's younger waves re-quantize first: the older waves take
   // the last range of each SIMD (the same partials, computed by other waves).
-  const WaveSegs ws = wave_segments(c_begin, c_end, w, WAVES, append,
+  const WaveSegs ws = wave_segments(c_begin, c_end, helper ? 0 : w, WAVES, append,
                                     VDT == kVF32 ? kFirstShare32F32 : kFirstShare32);
-  const int len1 = ws.p1 - ws.p0, len2 = ws.q1 - ws.q0, wlen = len1 + len2;
+  const int len1 = helper ? 0 : ws.p1 - ws.p0, len2 = helper ? 0 : ws.q1 - ws.q0;
+  const int wlen = len1 + len2;
   // The wave's i-th chunk.
   auto cidx = [&](int i) { return i < len1 ? ws.p0 + i : ws.q0 + (i - len1); };
   // Segment 1's partial is written when the loop reaches segment 2.
@@ -405,7 +420,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   // the append where the chunk's registers would not fit beside the rows
   // (head_dim 256, float32 values).
   constexpr bool kLateFirst = STEP && D == 256 && VDT == kVF32;
-  const bool rq_wave = STEP && append && w >= WAVES - 4;
+  const bool rq_wave = STEP && append && w >= WAVES + HW - 4;
   auto first_loads = [&]() {
     cm = meta_at(c);
     nm = meta_at(c + 1);
@@ -418,12 +433,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   }
   if (tid < D) q_s[tid] = qv;
   __syncthreads();
-  // With a token to append, the last four waves (with eight, the second wave
-  // of each SIMD, whose delay the first waves' streaming absorbs) each
-  // re-quantize a quarter of the open group's channels, then decode.
+  // With a token to append, the last four waves (the helpers, or with eight
+  // decode waves the second wave of each SIMD, whose delay the first waves'
+  // streaming absorbs) each re-quantize a quarter of the open group's
+  // channels, then decode what they own.
   if constexpr (STEP) {
     if (rq_wave) {
-      const int slice = w - (WAVES - 4);
+      const int slice = w - (WAVES + HW - 4);
       step_append<D, G::VEB>(a, b, hk, t_app, slice, lane, k_open, sz_open, v_open, pt_w[slice]);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0)
@@ -439,9 +455,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
   }
 
   // The last segment's partial; a range that this wave owns but that is
-  // empty (C with no chunks) gets the empty partial.
-  flush(seg_flush ? ws.s2 : ws.s1);
-  if (ws.s2 >= 0 && !seg_flush) flush(ws.s2);
+  // empty (C with no chunks) gets the empty partial. Helpers own none.
+  if (!helper) {
+    flush(seg_flush ? ws.s2 : ws.s1);
+    if (ws.s2 >= 0 && !seg_flush) flush(ws.s2);
+  }
   __syncthreads();
 
   double ms = -INFINITY;
@@ -523,7 +541,8 @@ hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hip
 #define FDI4_DEC(DD, VV, WW)                                                             \
   if (D == DD && v_dtype == VV && a.waves == WW) {                                       \
     if (a.step.k_new)                                                                    \
-      hipLaunchKernelGGL((decode_kernel<DD, VV, WW, true>), grid, dim3(WW * 64), 0, st, a); \
+      hipLaunchKernelGGL((decode_kernel<DD, VV, WW, true>), grid,                        \
+                         dim3((WW + helper_waves<WW, true>()) * 64), 0, st, a);              \
     else                                                                                 \
       hipLaunchKernelGGL((decode_kernel<DD, VV, WW, false>), grid, dim3(WW * 64), 0, st, a); \
     return hipGetLastError();                                                            \

@@ -296,16 +296,30 @@ class TestCABI:
         n = 8 * 32 * 4
         assert lib.fdi4_decode_workspace_bytes(8, 32, 128, 4) == n * 128 * 4 + n * 16
         assert lib.fdi4_decode_partials_bytes(8, 32, 128, 1) == 8 * 32 * (512 + 16)
-        # B8 x H32 (one q-head per kv-head) fills the chip with 8-wave
-        # workgroups: one split, no merge.
-        cache = capi.PagedCache(max_pages=128, page_rows=16, num_kv_heads=32, head_dim=128)
-        assert lib.fdi4_decode_num_splits(8, 32, cache) == 1
-        # T=512 (32 chunks): still 8 waves of 4 chunks and one split.
-        cache = capi.PagedCache(max_pages=32, page_rows=16, num_kv_heads=32, head_dim=128)
-        assert lib.fdi4_decode_num_splits(8, 32, cache) == 1
-        # B1 x H8 x 32768 tokens: 2048 chunks split 32 ways (2048 waves).
-        cache = capi.PagedCache(max_pages=2048, page_rows=16, num_kv_heads=8, head_dim=128)
-        assert lib.fdi4_decode_num_splits(1, 8, cache) == 32
+        # B8 x H32 (one q-head per kv-head), float32 values: 4-wave
+        # workgroups, one wave per SIMD, one split and no merge; float16
+        # values: 8-wave workgroups, one split.
+        for v_dtype in (capi.V_F32, capi.V_F16):
+            cache = capi.PagedCache(max_pages=128, page_rows=16, num_kv_heads=32, head_dim=128,
+                                    v_dtype=v_dtype)
+            assert lib.fdi4_decode_num_splits(8, 32, cache) == 1
+            # T=512 (32 chunks): still one split.
+            cache = capi.PagedCache(max_pages=32, page_rows=16, num_kv_heads=32, head_dim=128,
+                                    v_dtype=v_dtype)
+            assert lib.fdi4_decode_num_splits(8, 32, cache) == 1
+        # B1 x H8 x 32768 tokens: 2048 chunks split 32 ways (1024 waves of
+        # four-wave workgroups with float32 values, 2048 of eight with float16).
+        for v_dtype in (capi.V_F32, capi.V_F16):
+            cache = capi.PagedCache(max_pages=2048, page_rows=16, num_kv_heads=8, head_dim=128,
+                                    v_dtype=v_dtype)
+            assert lib.fdi4_decode_num_splits(1, 8, cache) == 32
+        # B1 x H8 x 1024 tokens (64 chunks): at least 4 chunks per wave, so
+        # four splits of four-wave workgroups (float32 values), two of eight.
+        cache = capi.PagedCache(max_pages=64, page_rows=16, num_kv_heads=8, head_dim=128)
+        assert lib.fdi4_decode_num_splits(1, 8, cache) == 4
+        cache = capi.PagedCache(max_pages=64, page_rows=16, num_kv_heads=8, head_dim=128,
+                                v_dtype=capi.V_F16)
+        assert lib.fdi4_decode_num_splits(1, 8, cache) == 2
         # GQA B8 x Hq32 x Hkv8 at D=128: four q-heads per workgroup, so 64
         # workgroups of 8 waves and 4 splits for ~2048 waves.
         cache = capi.PagedCache(max_pages=512, page_rows=16, num_kv_heads=8, head_dim=128)
@@ -331,8 +345,10 @@ class TestCABI:
         with capi.tuning(decode_waves=4, decode_heads_per_wg=2):
             assert lib.fdi4_get_tuning(waves) == 4
             assert lib.fdi4_get_tuning(capi.TUNE["decode_heads_per_wg"]) == 2
-            cache = capi.PagedCache(max_pages=32, page_rows=16, num_kv_heads=32, head_dim=128)
-            # 4 waves x 8 chunks each: B8 H32 now needs two splits for ~2048 waves.
+            cache = capi.PagedCache(max_pages=32, page_rows=16, num_kv_heads=32, head_dim=128,
+                                    v_dtype=capi.V_F16)
+            # 4 waves x 8 chunks each: B8 H32 with float16 values now needs two
+            # splits for ~2048 waves.
             assert lib.fdi4_decode_num_splits(8, 32, cache) == 2
         assert lib.fdi4_get_tuning(waves) == 0
         with pytest.raises(ValueError):
