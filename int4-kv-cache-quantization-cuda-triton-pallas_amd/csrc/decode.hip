@@ -6,11 +6,12 @@
 // page in logical order, empty pages skipped, out = acc / max(l, 1e-10).
 //
 // Work decomposition (split-K flash decoding):
-//   grid (num_splits, Hq, B); a workgroup of WAVES wave64s owns one split,
-//   a contiguous range of 16-row chunks of one (sequence, q-head); each SIMD
-//   takes a quarter of the range, cut into ranges of its two waves (about
-//   20:12 between the SIMD's older and younger wave with float32 values,
-//   18:14 with 16-bit values, the younger wave's last
+//   grid (num_splits, Hq, B); a workgroup of WAVES (4 or 8) wave64s owns
+//   one split, a contiguous range of 16-row chunks of one (sequence,
+//   q-head); each SIMD takes a quarter of the range, which its one wave
+//   computes (four waves) or which is cut into ranges of its two waves
+//   (eight: about 20:12 between the SIMD's older and younger wave with
+//   float32 values at D = 128, 18:14 otherwise, the younger wave's last
 //   chunks a range of their own, see wave_segments); every range keeps its
 //   own (m, l, acc) and the ranges are merged through LDS in a fixed order.
 //   (The fused serving step with four decode waves adds four helper waves
@@ -182,7 +183,8 @@ __global__ __launch_bounds__((WAVES + helper_waves<WAVES, STEP>()) * 64) void de
   // The serving step's younger waves re-quantize first: the older waves take
   // the last range of each SIMD (the same partials, computed by other waves).
   const WaveSegs ws = wave_segments(c_begin, c_end, helper ? 0 : w, WAVES, append,
-                                    VDT == kVF32 ? kFirstShare32F32 : kFirstShare32);
+                                    VDT == kVF32 && D == 128 ? kFirstShare32F32
+                                                             : kFirstShare32);
   const int len1 = helper ? 0 : ws.p1 - ws.p0, len2 = helper ? 0 : ws.q1 - ws.q0;
   const int wlen = len1 + len2;
   // The wave's i-th chunk.

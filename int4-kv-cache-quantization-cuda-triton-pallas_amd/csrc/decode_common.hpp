@@ -150,10 +150,12 @@ __device__ __forceinline__ int pages_of(const DecodeArgs& a, int T) {
 // 45.1 us), leaving one wave per SIMD, with half the loads in flight, for the
 // rest of the decode. The older wave therefore takes kFirstShare32 / 32 of
 // its SIMD's chunks (rounded to nearest) and the younger one the rest; the
-// per-head decode with float32 values gives it kFirstShare32F32 / 32 (in-process
-// A/B against 18/32, one box: B8 H32 T2048 -0.8 to -1.1 %, T1024 -2 %, T8192
-// -0.5 %, T512 and ragged B32 within 0.4 %; with 16-bit values 20/32 was
-// 1.5 % slower, 16/32 slower everywhere).
+// per-head decode with float32 values at D = 128 (512-byte value rows) gives
+// it kFirstShare32F32 / 32. In-process A/B against 18/32, one box, eight
+// waves: B8 H32 T2048 -0.8 to -1.1 %, T1024 -2 %, T8192 -0.5 %, B32 H32
+// T2048 -0.8 %, B64 H32 T4096 -0.3 %, ragged B32 within 0.5 %; slower with
+// other rows: float16 values at D = 128 +1.5 %, float32 at D = 64 +3 %, at
+// D = 256 +0.6 %; 16/32 slower everywhere.
 #ifndef FDI4_FIRST_SHARE32
 #define FDI4_FIRST_SHARE32 18
 #endif
