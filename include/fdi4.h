@@ -87,7 +87,9 @@ typedef struct fdi4_paged_cache {
  *   FDI4_TUNE_DECODE_VECTOR_ONLY   1: grouped-head decodes at head_dim 64/128
  *                                  run on the vector kernels instead of the
  *                                  int8 matrix-core kernel
- *   FDI4_TUNE_DECODE_WAVES         4 or 8 wave64s per decode workgroup
+ *   FDI4_TUNE_DECODE_WAVES         4 or 8 decode wave64s per workgroup (the
+ *                                  fused serving step adds 4 re-quantizing
+ *                                  waves to a 4-wave workgroup)
  *   FDI4_TUNE_DECODE_HEADS_PER_WG  cap on q-heads per decode workgroup: 1
  *                                  (per-head kernel), 2, 4 or 8
  *   FDI4_TUNE_DECODE_TARGET_WAVES  resident waves the split count aims for

@@ -383,11 +383,11 @@ class INT4PagedSequenceCache:
         returns [B, Hq, D] in the query's dtype.
         No host bookkeeping happens, so the call can be captured in a HIP
         graph and replayed. Each graph launch leaves the GPU idle for a few
-        microseconds before the graph's first kernel (about 4.7 us on
+        microseconds before the graph's first kernel (about 4.3-4.7 us on
         MI355X, measured: a graph holding one B8 H32 T2048 step replays in
-        60.0 us against 55.3 us eager), so capture it together with the rest
+        58.2 us against 53.9 us eager), so capture it together with the rest
         of the token step (the other layers' caches) or several steps per
-        graph (55.6 us per step from a graph of eight). The pages must already
+        graph (53.6 us per step from a graph of eight). The pages must already
         be mapped (reserve), and
         lengths() reflects the steps only after sync_lengths(); append(),
         prefill(), reserve() and free() read the device lengths first.
