@@ -81,12 +81,22 @@ __device__ __forceinline__ void step_append(const DecodeArgs& a, int b, int hk, 
 }
 
 // The fused serving step's length advance: every workgroup of sequence b
-// counts its arrival when it has finished (each read the old length at its
-// start); the last to arrive writes the new length and clears the counter for
-// the next step. A relaxed device-scope atomic: the count is all the
-// arrivals need to agree on.
-__device__ __forceinline__ void step_arrive(const DecodeArgs& a, int b, int len_after) {
-  if (threadIdx.x != 0) return;
+// counts its arrival once all its waves have read the old length; the last to
+// arrive writes the new length and clears the counter for the next step. A
+// relaxed device-scope atomic: the count is all the arrivals need to agree
+// on. Called by one wave (its lane 0): with helper waves and 16-bit values the
+// first helper, once its re-quantization is done (after the first workgroup
+// barrier, every wave having used the length before it), so that the
+// atomic's round trip passes under the decode; otherwise wave 0 at the
+// workgroup's end. (On a streaming wave a returning atomic would hold up the
+// waits of every later chunk load, which the hardware counts in order. In
+// process A/B of the step, one box: the early count from the helper gains with
+// 16-bit values, B8 H32 D128 float16 38.9 -> 37.8 us, bfloat16 37.3 -> 36.5,
+// D64 float16 28.1 -> 23.8 with the helper waves, and loses with float32
+// values, D128 53.3-54.0 -> 54.2-54.3 us.)
+__device__ __forceinline__ void step_arrive(const DecodeArgs& a, int b, int lane,
+                                            int len_after) {
+  if (lane != 0) return;
   const int n = gridDim.x * gridDim.y;
   const int prev =
       __hip_atomic_fetch_add(a.step.arrive + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -109,19 +119,25 @@ __device__ __forceinline__ void merge_term(double m, double ms, float acc, doubl
 }
 
 // Waves of a decode workgroup that only re-quantize: the fused serving step
-// with four decode waves adds four, which re-quantize the open group while
-// the decode waves stream (with eight decode waves the younger four do it
-// first, then decode).
-template <int WAVES, bool STEP>
+// adds four, which re-quantize the open group while the decode waves stream,
+// with four decode waves, and with eight where three waves per SIMD fit in
+// the registers (16-bit values at head_dim <= 128, float32 values at 64).
+// Otherwise (eight decode waves at head_dim 256, or float32 values at 128)
+// the younger four decode waves re-quantize first, then decode.
+template <int D, int VDT, int WAVES, bool STEP>
 constexpr int helper_waves() {
-  return STEP && WAVES == 4 ? 4 : 0;
+  if (!STEP) return 0;
+  if (WAVES == 4) return 4;
+  return (VDT == kVF32 ? D == 64 : D <= 128) ? 4 : 0;
 }
 
 template <int D, int VDT, int WAVES, bool STEP>
-__global__ __launch_bounds__((WAVES + helper_waves<WAVES, STEP>()) * 64) void decode_kernel(
-    DecodeArgs a) {
+__global__ __launch_bounds__((WAVES + helper_waves<D, VDT, WAVES, STEP>()) * 64) void
+decode_kernel(DecodeArgs a) {
   using G = Geo<D, VDT>;
-  constexpr int HW = helper_waves<WAVES, STEP>();
+  constexpr int HW = helper_waves<D, VDT, WAVES, STEP>();
+  // Where the serving step counts its arrival (step_arrive).
+  constexpr bool kEarlyArrive = STEP && HW > 0 && VDT != kVF32;
   constexpr int NT = (WAVES + HW) * 64;
 
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -169,6 +185,10 @@ __global__ __launch_bounds__((WAVES + helper_waves<WAVES, STEP>()) * 64) void de
     t_app = fits ? raw : -1;
     T = fits ? raw + 1 : min(max(raw, 0), cap);
     len_after = fits ? raw + 1 : raw;
+    // Every wave holds the length read before the first workgroup barrier,
+    // after which a helper wave counts the workgroup's arrival (step_arrive);
+    // a helper would otherwise first use it after the barrier.
+    asm volatile("" ::"s"(raw));
   } else {
     T = seq_len_of(a, b);
   }
@@ -180,9 +200,10 @@ __global__ __launch_bounds__((WAVES + helper_waves<WAVES, STEP>()) * 64) void de
   const int n_chunks = pages_of(a, T) * cpp;
   const int c_begin = split * a.chunks_per_split;
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
-  // The serving step's younger waves re-quantize first: the older waves take
-  // the last range of each SIMD (the same partials, computed by other waves).
-  const WaveSegs ws = wave_segments(c_begin, c_end, helper ? 0 : w, WAVES, append,
+  // Where the serving step's younger decode waves re-quantize first, the
+  // older waves take the last range of each SIMD (the same partials,
+  // computed by other waves).
+  const WaveSegs ws = wave_segments(c_begin, c_end, helper ? 0 : w, WAVES, append && HW == 0,
                                     VDT == kVF32 && D == 128 ? kFirstShare32F32
                                                              : kFirstShare32);
   const int len1 = helper ? 0 : ws.p1 - ws.p0, len2 = helper ? 0 : ws.q1 - ws.q0;
@@ -448,6 +469,9 @@ __global__ __launch_bounds__((WAVES + helper_waves<WAVES, STEP>()) * 64) void de
         __hip_atomic_fetch_add(&open_done, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       if (kLateFirst && has_work) first_loads();
     }
+    if constexpr (kEarlyArrive) {
+      if (w == WAVES) step_arrive(a, b, lane, len_after);
+    }
   }
   if (has_work) {
     while (true) {
@@ -491,7 +515,9 @@ __global__ __launch_bounds__((WAVES + helper_waves<WAVES, STEP>()) * 64) void de
     a.ws_ml[2 * pi + 1] = (double)l;
   }
   hand_back_length(a, b);
-  if constexpr (STEP) step_arrive(a, b, len_after);
+  if constexpr (STEP && !kEarlyArrive) {
+    if (w == 0) step_arrive(a, b, lane, len_after);
+  }
 }
 
 // Log-sum-exp merge of the split partials: grid (Hq, B), one thread per
@@ -544,7 +570,7 @@ hipError_t launch_decode(const DecodeArgs& a, int D, int v_dtype, int batch, hip
   if (D == DD && v_dtype == VV && a.waves == WW) {                                       \
     if (a.step.k_new)                                                                    \
       hipLaunchKernelGGL((decode_kernel<DD, VV, WW, true>), grid,                        \
-                         dim3((WW + helper_waves<WW, true>()) * 64), 0, st, a);              \
+                         dim3((WW + helper_waves<DD, VV, WW, true>()) * 64), 0, st, a);      \
     else                                                                                 \
       hipLaunchKernelGGL((decode_kernel<DD, VV, WW, false>), grid, dim3(WW * 64), 0, st, a); \
     return hipGetLastError();                                                            \
