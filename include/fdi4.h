@@ -89,7 +89,8 @@ typedef struct fdi4_paged_cache {
  *                                  int8 matrix-core kernel
  *   FDI4_TUNE_DECODE_WAVES         4 or 8 decode wave64s per workgroup (the
  *                                  fused serving step adds 4 re-quantizing
- *                                  waves to a 4-wave workgroup)
+ *                                  waves to 4-wave workgroups, and to 8-wave
+ *                                  ones where registers allow)
  *   FDI4_TUNE_DECODE_HEADS_PER_WG  cap on q-heads per decode workgroup: 1
  *                                  (per-head kernel), 2, 4 or 8
  *   FDI4_TUNE_DECODE_TARGET_WAVES  resident waves the split count aims for
