@@ -420,7 +420,12 @@ def decode_launchers(sets, splits):
     return S, step, decode_only
 
 
-def interleaved_us(fa, fb, rounds=10, block=20):
+# Launches per block of the alternating check: each block starts on the other
+# input sets, so a longer block leaves that switch a smaller share of it.
+INTERLEAVE_BLOCK = 40
+
+
+def interleaved_us(fa, fb, rounds=10, block=INTERLEAVE_BLOCK):
     """Per-launch time of two launch sequences measured in alternating blocks
     (A, B, A, B, ...) of `block` back-to-back launches after settle(), one
     event between blocks and one synchronize at the end, so both see the same
@@ -1269,7 +1274,7 @@ def main():
                                   4),
                 "interleaved": {"anchor_us": round(base_us, 3), "plus_1_us": round(odd_us, 3),
                                 "ratio": round(odd_us / base_us, 4), "rounds": 10,
-                                "launches_per_block": 20,
+                                "launches_per_block": INTERLEAVE_BLOCK,
                                 "anchor_vs_headline": round(base_us / win_us, 4)}},
         },
         "roofline": roofline,
