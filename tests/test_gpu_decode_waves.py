@@ -72,15 +72,20 @@ def test_either_wave_count_matches_the_oracle(batch, heads, d, lens, vdt):
 
 
 @pytest.mark.parametrize("waves", [4, 8])
-def test_fused_step_equals_append_and_decode_at_either_wave_count(waves):
-    """B4 H8 D128 float32 values from 600 tokens, one split (so the step is
-    one launch), 12 steps across a scale-group boundary: the one-launch step
-    (with four decode waves, plus four helpers) against the append, the
-    length increment and the decode of a twin cache."""
+@pytest.mark.parametrize("vdt,d", [("float32", 128), ("float16", 128), ("float32", 64),
+                                   ("bfloat16", 256)])
+def test_fused_step_equals_append_and_decode_at_either_wave_count(waves, vdt, d):
+    """B4 H8 from 600 tokens, one split (so the step is one launch), 12 steps
+    across a scale-group boundary: the one-launch step against the append,
+    the length increment and the decode of a twin cache. The step's
+    workgroup: four decode waves plus four helpers; eight decode waves plus
+    four helpers (16-bit values at D = 128, float32 at D = 64; the first
+    helper counts the arrival with 16-bit values); eight decode waves whose
+    younger four re-quantize (float32 at D = 128, D = 256)."""
     import torch
     from flash_decode_int4 import capi
     from flash_decode_int4.vllm_integration import INT4PagedSequenceCache
-    B, H, D, T0 = 4, 8, 128, 600
+    B, H, D, T0 = 4, 8, d, 600
     g = torch.Generator(device="cuda")
     g.manual_seed(waves)
     k = torch.randn(B, H, T0, D, device="cuda", generator=g)
@@ -88,7 +93,8 @@ def test_fused_step_equals_append_and_decode_at_either_wave_count(waves):
     caches = []
     for _ in range(2):
         c = INT4PagedSequenceCache(num_pages=B * (T0 // 16 + 4), num_kv_heads=H, head_dim=D,
-                                   max_seqs=B, max_seq_len=T0 + 40, group_rows=128)
+                                   max_seqs=B, max_seq_len=T0 + 40, group_rows=128,
+                                   value_dtype=vdt)
         c.prefill(k, v, [T0] * B)
         c.reserve(B, 12)
         caches.append(c)
@@ -96,7 +102,7 @@ def test_fused_step_equals_append_and_decode_at_either_wave_count(waves):
     with capi.tuning(decode_waves=waves, decode_target_waves=1):
         for i in range(12):
             kn = torch.randn(B, H, D, device="cuda", generator=g)
-            vn = torch.randn(B, H, D, device="cuda", generator=g)
+            vn = torch.randn(B, H, D, device="cuda", generator=g).to(getattr(torch, vdt))
             q = torch.randn(B, H, D, device="cuda", generator=g)
             out_new = new.step(kn, vn, q)
             old.append(kn, vn)
