@@ -185,10 +185,10 @@ decode_kernel(DecodeArgs a) {
     t_app = fits ? raw : -1;
     T = fits ? raw + 1 : min(max(raw, 0), cap);
     len_after = fits ? raw + 1 : raw;
-    // Every wave holds the length read before the first workgroup barrier,
-    // after which a helper wave counts the workgroup's arrival (step_arrive);
-    // a helper would otherwise first use it after the barrier.
-    asm volatile("" ::"s"(raw));
+    // Where a helper wave counts the workgroup's arrival after the first
+    // workgroup barrier (step_arrive), every wave holds the length read
+    // before that barrier; a helper would otherwise first use it after it.
+    if constexpr (kEarlyArrive) asm volatile("" ::"s"(raw));
   } else {
     T = seq_len_of(a, b);
   }
