@@ -663,7 +663,8 @@ def time_other_paths(args):
     return out
 
 
-def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8, graphs=True):
+def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8, graphs=True,
+                     max_seq_len=None):
     """The serving loop's step on the sequence cache (fp32 values, B sequences
     of H heads around T tokens): append one token per (sequence, kv-head),
     decode over the advanced lengths, advance them -- one launch when each
@@ -681,8 +682,9 @@ def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8, graphs=True)
     G = 128
     T0 = T - G // 2
     rounds = 4
+    cap = max_seq_len or T0 + G
     cache = INT4PagedSequenceCache(num_pages=B * ((T0 + G) // 16 + 2), num_kv_heads=H,
-                                   head_dim=D, max_seqs=B, max_seq_len=T0 + G, group_rows=G)
+                                   head_dim=D, max_seqs=B, max_seq_len=cap, group_rows=G)
     g = torch.Generator(device="cuda")
     g.manual_seed(3)
     k = torch.randn(B, H, T0, D, device="cuda", generator=g)
@@ -743,7 +745,7 @@ def time_decode_step(args, B=8, H=32, D=128, T=2048, graph_steps=8, graphs=True)
     dec = median([timed(lambda: cache.decode(q), 20) / 20 for _ in range(rounds)])
     res = {"workload": f"B{B} H{H} D{D}, fp32 values: append + decode + length advance per "
                        f"step, steps from {T0} to {T0 + G} tokens (one {G}-token scale group, "
-                       f"mean {T - 0.5})",
+                       f"mean {T - 0.5}), a cache of {cap} tokens per sequence",
            "eager_us": round(median(eager), 3),
            "graph_replay_us": round(median(rep_1), 3) if graphs else None,
            f"graph_{graph_steps}_steps_replay_us_per_step":

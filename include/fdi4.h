@@ -278,14 +278,16 @@ int fdi4_decode_paged_advance(const void* query, int query_dtype, int batch, int
  * fdi4_append_paged, that length update and fdi4_decode_paged_ex, bit for
  * bit. Every argument is checked before anything is enqueued: a rejected
  * call (hipErrorInvalidValue) leaves the cache unchanged.
- * When each (sequence, kv-head) is one decode workgroup (num_q_heads ==
- * num_kv_heads and a single split) this is ONE launch: every workgroup
- * appends its own token and re-quantizes the open group before it decodes,
- * and the last workgroup of a sequence to finish advances its length
- * (counters: int32 [batch], zero before the first call, left zero by every
- * call). Otherwise it is fdi4_append_paged_advance into lens_next (int32
- * [batch] scratch) and fdi4_decode_paged_advance back, with the library's
- * split count (workspace of fdi4_decode_workspace_bytes). counters,
+ * With num_q_heads == num_kv_heads and splits of whole scale groups (a single
+ * split, or a split length that is a multiple of a group's 16-row chunks)
+ * this is ONE launch, then the split merge when there are several: the
+ * workgroup of the split that holds the open group appends its token and
+ * re-quantizes the group before it decodes it, and the last workgroup of a
+ * sequence to count itself advances its length (counters: int32 [batch],
+ * zero before the first call, left zero by every call). Otherwise it is
+ * fdi4_append_paged_advance into lens_next (int32 [batch] scratch) and
+ * fdi4_decode_paged_advance back. Both use the library's split count
+ * (workspace of fdi4_decode_workspace_bytes). counters,
  * lens_next and cache->seq_lens must not overlap. No counterpart in the
  * reference, whose cache appends on the host. */
 int fdi4_decode_step(const void* query, int query_dtype, int batch, int num_q_heads,

@@ -671,20 +671,27 @@ int fdi4_decode_step(const void* query, int query_dtype, int batch, int num_q_he
                         cache, 0, &a);
   if (rc != hipSuccess) return rc;
   if (!out || !valid_elem_dtype(out_dtype)) return hipErrorInvalidValue;
-  // One workgroup per (sequence, kv-head): the append fuses into the decode
-  // (whose reads of a group's staging rows take 32-bit byte offsets).
-  const bool fused = a.num_splits == 1 && !a.mfma && a.heads_per_wg == 1 && a.hq_per_kv == 1 &&
+  // One q-head per kv-head and splits of whole scale groups (one split, or
+  // chunks_per_split a multiple of a group's chunks, so that the open group
+  // lies in one split): the append fuses into the decode (whose reads of a
+  // group's staging rows take 32-bit byte offsets); with several splits the
+  // merge follows it.
+  const int group_chunks = cache->pages_per_group * ceil_div(cache->page_rows, 16);
+  const bool fused = !a.mfma && a.heads_per_wg == 1 && a.hq_per_kv == 1 &&
+                     (a.num_splits == 1 || a.chunks_per_split % group_chunks == 0) &&
                      (int64_t)group_rows * st_row_stride * 4 <= INT32_MAX;
+  // Both forms check the workspace before anything is launched, so a rejected
+  // call leaves the cache as it was.
+  if (a.num_splits > 1 &&
+      (!workspace || !aligned(workspace, kAlign) ||
+       workspace_bytes < decode_ws_bytes(batch, num_q_heads, cache->head_dim, a.num_splits)))
+    return hipErrorInvalidValue;
   if (!fused) {
     // Two launches: the append writes the advanced lengths to lens_next, the
     // decode attends over them and copies them back to the cache's lengths.
     // Everything the decode checks is checked before the append writes the
-    // cache, so a rejected call leaves the cache as it was. The decode's plan
-    // (and so its split count and workspace) depends on the shapes only.
-    if (a.num_splits > 1 &&
-        (!workspace || !aligned(workspace, kAlign) ||
-         workspace_bytes < decode_ws_bytes(batch, num_q_heads, cache->head_dim, a.num_splits)))
-      return hipErrorInvalidValue;
+    // cache. The decode's plan (and so its split count and workspace)
+    // depends on the shapes only.
     ap.lens_next = lens_next;
     hipError_t e = fdi4::launch_append_paged(ap, cache->head_dim, group_rows, batch,
                                              cache->num_kv_heads, stream);
@@ -700,7 +707,11 @@ int fdi4_decode_step(const void* query, int query_dtype, int batch, int num_q_he
   a.out_dtype = out_dtype;
   a.o_b = out_batch_stride;
   a.o_h = out_head_stride;
-  a.final_out = 1;
+  a.final_out = a.num_splits == 1 ? 1 : 0;
+  if (a.num_splits > 1) {
+    rc = carve_partials(workspace, workspace_bytes, batch, num_q_heads, cache->head_dim, &a);
+    if (rc != hipSuccess) return rc;
+  }
   fdi4::StepAppend& st = a.step;
   st.k_new = k_new;
   st.kn_b = ap.kn_b;
@@ -715,7 +726,10 @@ int fdi4_decode_step(const void* query, int query_dtype, int batch, int num_q_he
   st.group_rows = group_rows;
   st.arrive = counters;
   st.lens = const_cast<int32_t*>(lens);
-  return fdi4::launch_decode(a, cache->head_dim, cache->v_dtype, batch, stream);
+  hipError_t e = fdi4::launch_decode(a, cache->head_dim, cache->v_dtype, batch, stream);
+  if (e != hipSuccess || a.num_splits == 1) return e;
+  return fdi4::launch_merge(a.ws_acc, a.ws_ml, batch, num_q_heads, cache->head_dim, a.num_splits,
+                            out, out_dtype, out_batch_stride, out_head_stride, stream);
 }
 
 int fdi4_decode_paged_partials(const float* query, int batch, int num_q_heads,

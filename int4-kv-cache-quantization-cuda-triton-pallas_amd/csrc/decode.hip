@@ -200,10 +200,15 @@ decode_kernel(DecodeArgs a) {
   const int n_chunks = pages_of(a, T) * cpp;
   const int c_begin = split * a.chunks_per_split;
   const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
+  // The split that holds the open group re-quantizes it (with several splits
+  // the host fuses the append only where every split holds whole scale
+  // groups, so the group lies in one split); the others only decode.
+  const int c_open = open_g * a.pages_per_group * cpp;
+  const bool owns_open = append && c_open >= c_begin && c_open < c_begin + a.chunks_per_split;
   // Where the serving step's younger decode waves re-quantize first, the
   // older waves take the last range of each SIMD (the same partials,
   // computed by other waves).
-  const WaveSegs ws = wave_segments(c_begin, c_end, helper ? 0 : w, WAVES, append && HW == 0,
+  const WaveSegs ws = wave_segments(c_begin, c_end, helper ? 0 : w, WAVES, owns_open && HW == 0,
                                     VDT == kVF32 && D == 128 ? kFirstShare32F32
                                                              : kFirstShare32);
   const int len1 = helper ? 0 : ws.p1 - ws.p0, len2 = helper ? 0 : ws.q1 - ws.q0;
@@ -443,7 +448,7 @@ decode_kernel(DecodeArgs a) {
   // the append where the chunk's registers would not fit beside the rows
   // (head_dim 256, float32 values).
   constexpr bool kLateFirst = STEP && D == 256 && VDT == kVF32;
-  const bool rq_wave = STEP && append && w >= WAVES + HW - 4;
+  const bool rq_wave = STEP && owns_open && w >= WAVES + HW - 4;
   auto first_loads = [&]() {
     cm = meta_at(c);
     nm = meta_at(c + 1);

@@ -417,8 +417,9 @@ class INT4PagedSequenceCache:
                                           self.group_rows // self.page_rows,
                                           self.max_pages_per_seq, int(num_splits),
                                           self.seq_lens[:B])
-        # One launch when each (sequence, kv-head) is one decode workgroup,
-        # two otherwise (fdi4_decode_step decides).
+        # One launch (plus the split merge) with one q-head per kv-head when
+        # the splits hold whole scale groups, two otherwise (fdi4_decode_step
+        # decides).
         return load_binding().decode_step(query, k_new, v_new, self.k_stage, self.k_pages,
                                           self.v_pages, self.k_scale, self.k_zp,
                                           self.page_table, self.seq_lens, self.group_rows,

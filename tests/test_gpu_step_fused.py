@@ -195,17 +195,19 @@ def _reference_step(c, kn, vn, q, after, splits):
     return c.decode(q, num_splits=splits)
 
 
-@pytest.mark.parametrize("form", ["one_launch", "two_launch"])
+@pytest.mark.parametrize("form", ["one_launch", "split_fused", "two_launch"])
 def test_step_lengths_outside_the_cache(form):
     """Lengths below 0 and above the cache's capacity: no token is appended,
     the length is left as read, and the decode attends over it clamped to
-    [0, capacity] -- in the one-launch step, in the two-launch step, and in
+    [0, capacity] -- in the one-launch step, in the fused step over two splits
+    (then the merge), in the two-launch step (two q-heads per kv-head), and in
     the append kernel + decode form, bit for bit (outputs, pages, scales,
     values, staging rows, lengths)."""
     import torch
     from flash_decode_int4 import capi
     from flash_decode_int4._lib import load_binding
     B, H, D = 5, 2, 128
+    HQ = 2 * H if form == "two_launch" else H
     lens0 = [100, 40, 200, 17, 511]
     (new, old), g = _twins(B, H, D, lens0, 16, 128, "float32", 512, 71)
     cap = new.max_pages_per_seq * new.page_rows
@@ -216,15 +218,16 @@ def test_step_lengths_outside_the_cache(form):
         c.seq_lens[:B] = torch.tensor(raw, dtype=torch.int32, device="cuda")
     kn = torch.randn(B, H, D, device="cuda", generator=g)
     vn = torch.randn(B, H, D, device="cuda", generator=g)
-    q = torch.randn(B, H, D, device="cuda", generator=g)
+    q = torch.randn(B, HQ, D, device="cuda", generator=g)
     # One split takes the one-launch step; four-wave workgroups and a high
-    # wave target give two splits (32 chunks of 4 per wave), so the
-    # two-launch step.
+    # wave target give two splits (32 chunks of 4 per wave, 16 per split:
+    # two whole 128-row groups each), so the fused step and the merge; with
+    # two q-heads per kv-head the step is the append kernel, then the decode.
     tune = {"decode_waves": 4,
             "decode_target_waves": 1 if form == "one_launch" else 4096}
     C = load_binding()
     with capi.tuning(**tune):
-        splits = int(C.decode_num_splits(B, H, H, D, new.max_pages_per_seq, 16))
+        splits = int(C.decode_num_splits(B, HQ, H, D, new.max_pages_per_seq, 16))
         assert (splits == 1) == (form == "one_launch")
         out_new = load_step(new, kn, vn, q)
         out_old = _reference_step(old, kn, vn, q, after, splits)
