@@ -1252,7 +1252,10 @@ def main():
     progress("timing the other decode paths and the serving step")
     other = time_other_paths(args)
     other["decode_step"] = time_decode_step(args)
-    other["decode_step_small"] = time_decode_step(args, B=1, H=8, D=128, T=1024)
+    # One sequence in a 2048-token cache: four splits of whole scale groups,
+    # so the step is one launch and the merge.
+    other["decode_step_small"] = time_decode_step(args, B=1, H=8, D=128, T=1024,
+                                                  max_seq_len=2048)
 
     q_us = qt
 
