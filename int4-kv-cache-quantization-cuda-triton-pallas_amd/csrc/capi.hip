@@ -29,6 +29,7 @@ using fdi4::QuantPagedArgs;
 // FDI4_TUNE_DECODE_WAVES and FDI4_TUNE_DECODE_TARGET_WAVES override the choice.
 constexpr int kTargetWaves = 2048;
 constexpr int kMinChunksPerWave = 4;
+constexpr int kMaxGroupedSplits = 8;
 constexpr size_t kAlign = 256;
 
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
@@ -158,7 +159,14 @@ DecodePlan plan_decode(int batch, int hq, int hq_per_kv, int d, int v_dtype, int
       tw > 0 ? tw : (per_simd && p.waves == 4 ? kTargetWaves / 2 : kTargetWaves);
   const int64_t per_split = (int64_t)batch * (hq / p.heads_per_wg) * p.waves;
   const int s = (int)((target + per_split - 1) / per_split);
-  const int smax = std::max(1, chunks / (p.waves * kMinChunksPerWave));
+  int smax = std::max(1, chunks / (p.waves * kMinChunksPerWave));
+  // Grouped heads (several q-heads per workgroup, more work per chunk) split
+  // down to one chunk per wave, up to eight splits (one merge round): in
+  // process A/B against four chunks per wave, one box: B1 Hkv8 Hq32 T1024
+  // 15.3 -> 12.0 us (8 splits against 2), B2 T2048 16.1 -> 13.8 (8 against
+  // 4), D64 B2 Hq64 T2048 14.9 -> 13.4, the shared-stream call of 8 x 256
+  // rows 19.1 -> 17.0; 16 and 32 splits were slower (B1 T4096 16.2 -> 22.3).
+  if (p.heads_per_wg > 1) smax = std::max(smax, std::min(chunks / p.waves, kMaxGroupedSplits));
   p.splits = std::max(1, std::min(s, smax));
   return p;
 }
