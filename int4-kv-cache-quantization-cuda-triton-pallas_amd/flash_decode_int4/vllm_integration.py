@@ -5,14 +5,15 @@ Drop-in for the reference's src/vllm_integration.py:29-102
 ``free_block``, ``decode_attention(query, block_table)`` and
 ``memory_stats``), backed by a device page pool instead of host dicts:
 
-  keys    uint8 [num_blocks, block_size, Dp/2]  nibble-packed (Dp = head_dim
+  keys    uint8 [slots, block_size, Dp/2]  nibble-packed (Dp = head_dim
           padded to 64/128/256; padding channels hold nibble 0, scale 0)
-  values  float16 [num_blocks, block_size, Dp]  (the reference stores fp16 V)
-  scales  float32 [num_blocks, Dp] and zero-points, one group per block
+  values  float16 [slots, block_size, Dp]  (the reference stores fp16 V)
+  scales  float32 [slots, Dp] and zero-points, a block's group in each of
+          its slots
 
 ``write_block`` quantizes the block on the GPU as ONE scale group over its
 rows (reference :48-56, bit-exact with quantize_int4_ref) and writes the
-packed rows straight into the block's slot. ``decode_attention`` runs the
+packed rows into the block's slots (one per block_size rows; any block id). ``decode_attention`` runs the
 packed-native split-K decode over the block table with no host unpack (the
 reference unpacks every block on the host, :62-78). As in the reference all
 queries attend the same block table.
@@ -63,7 +64,16 @@ class _SlotView:
 
 
 class INT4PagedKVCache:
-    """Paged KV cache: nibble-packed INT4 keys and fp16 values in HBM."""
+    """Paged KV cache: nibble-packed INT4 keys and fp16 values in HBM.
+
+    The device pool is made of slots of block_size rows. A block -- any
+    block id and any row count, as the reference's dictionaries allow --
+    takes ceil(rows / block_size) slots; the pool starts with num_blocks
+    slots and grows when the written blocks need more. Every slot of a block
+    carries the block's scale and zero-point (one group over all its rows,
+    as the reference quantizes a block), so the decode reads a long block
+    as consecutive pages of one group, in row order.
+    """
 
     def __init__(self, num_blocks: int, block_size: int, head_dim: int):
         import torch
@@ -77,16 +87,44 @@ class INT4PagedKVCache:
         self.head_dim = head_dim
         self._dp = ops._padded_dim(head_dim)
         dev = torch.device("cuda")
+        self._cap = num_blocks
         self._k = torch.zeros(num_blocks, block_size, self._dp // 2, dtype=torch.uint8, device=dev)
         self._v = torch.zeros(num_blocks, block_size, self._dp, dtype=torch.float16, device=dev)
         self._s = torch.zeros(num_blocks, self._dp, dtype=torch.float32, device=dev)
         self._z = torch.zeros(num_blocks, self._dp, dtype=torch.float32, device=dev)
+        self._slots = {}                                  # block_id -> pool slots, in row order
+        self._free = list(range(num_blocks - 1, -1, -1))  # pop() hands out slot 0 first
         self.lens = {}
         pk = (head_dim + 1) // 2
-        self.k_packed = _SlotView(self, lambda b: self._k[b, :self.lens[b], :pk].cpu().numpy())
-        self.k_scale = _SlotView(self, lambda b: self._s[b, :head_dim].cpu().numpy())
-        self.k_zp = _SlotView(self, lambda b: self._z[b, :head_dim].cpu().numpy())
-        self.v = _SlotView(self, lambda b: self._v[b, :self.lens[b], :head_dim].cpu().numpy())
+        self.k_packed = _SlotView(self, lambda b: self._rows(self._k, b)[:, :pk].cpu().numpy())
+        self.k_scale = _SlotView(self, lambda b: self._s[self._slots[b][0], :head_dim].cpu().numpy())
+        self.k_zp = _SlotView(self, lambda b: self._z[self._slots[b][0], :head_dim].cpu().numpy())
+        self.v = _SlotView(self, lambda b: self._rows(self._v, b)[:, :head_dim].cpu().numpy())
+
+    def _pieces(self, block_id):
+        """(slot, rows) of each slot of a block, in row order."""
+        n, bs = self.lens[block_id], self.block_size
+        return [(s, min(bs, n - j * bs)) for j, s in enumerate(self._slots[block_id])]
+
+    def _rows(self, pool, block_id):
+        import torch
+        return torch.cat([pool[s, :r] for s, r in self._pieces(block_id)])
+
+    def _take(self, n):
+        """n free slots; the pool grows (at least doubling) when too few are free."""
+        import torch
+        short = n - len(self._free)
+        if short > 0:
+            cap = max(self._cap + short, 2 * self._cap)
+            for name in ("_k", "_v", "_s", "_z"):
+                old = getattr(self, name)
+                new = torch.zeros((cap,) + tuple(old.shape[1:]), dtype=old.dtype,
+                                  device=old.device)
+                new[:self._cap] = old
+                setattr(self, name, new)
+            self._free = list(range(cap - 1, self._cap - 1, -1)) + self._free
+            self._cap = cap
+        return [self._free.pop() for _ in range(n)]
 
     def write_block(self, block_id: int, k_block: np.ndarray, v_block: np.ndarray) -> None:
         """Quantize (one group over the block's rows), pack and store one block."""
@@ -96,21 +134,39 @@ class INT4PagedKVCache:
         if np.shape(k_block) != np.shape(v_block):
             raise AssertionError(f"k_block shape {np.shape(k_block)} != v_block shape "
                                  f"{np.shape(v_block)}")
+        if np.ndim(k_block) != 2 or np.shape(k_block)[1] != self.head_dim:
+            raise ValueError(f"block must be [rows, {self.head_dim}], got {np.shape(k_block)}")
         rows, d = np.shape(k_block)
-        if d != self.head_dim:
-            raise ValueError(f"block has head_dim {d}, cache has {self.head_dim}")
-        if not 1 <= rows <= self.block_size:
-            raise ValueError(f"block has {rows} rows; 1..{self.block_size} fit in a block")
-        if not 0 <= block_id < self.num_blocks:
-            raise ValueError(f"block_id {block_id} outside [0, {self.num_blocks})")
-        k_t = torch.from_numpy(np.ascontiguousarray(k_block, dtype=np.float32)).cuda()
-        load_binding().quantize_rows_into(k_t, self._k[block_id, :rows], self._s[block_id],
-                                          self._z[block_id], True)
-        v16 = np.ascontiguousarray(np.asarray(v_block).astype(np.float16))
-        self._v[block_id, :rows, :d] = torch.from_numpy(v16).cuda()
+        if rows < 1:
+            raise ValueError("a block needs at least one row")
+        dev = torch.device("cuda")
+        # Everything that can fail happens before the cache changes.
+        k_t = torch.from_numpy(np.ascontiguousarray(k_block, dtype=np.float32)).to(dev)
+        kq = torch.zeros(rows, self._dp // 2, dtype=torch.uint8, device=dev)
+        sc = torch.zeros(self._dp, dtype=torch.float32, device=dev)
+        zp = torch.zeros(self._dp, dtype=torch.float32, device=dev)
+        load_binding().quantize_rows_into(k_t, kq, sc, zp, True)
+        v_t = torch.from_numpy(np.ascontiguousarray(np.asarray(v_block).astype(np.float16)))
+        v_t = v_t.to(dev)
+        old = self._slots.pop(block_id, None)
+        if old:
+            self._free.extend(reversed(old))
+        self.lens.pop(block_id, None)
+        slots = self._take(-(-rows // self.block_size))
+        bs = self.block_size
+        for j, s in enumerate(slots):
+            r0, r1 = j * bs, min(rows, (j + 1) * bs)
+            self._k[s, :r1 - r0] = kq[r0:r1]
+            self._v[s, :r1 - r0, :d] = v_t[r0:r1]
+            self._s[s] = sc
+            self._z[s] = zp
+        self._slots[block_id] = slots
         self.lens[block_id] = rows
 
     def free_block(self, block_id: int) -> None:
+        slots = self._slots.pop(block_id, None)
+        if slots:
+            self._free.extend(reversed(slots))
         self.lens.pop(block_id, None)
 
     def decode_attention(self, query: np.ndarray, block_table: List[int]) -> np.ndarray:
@@ -120,18 +176,20 @@ class INT4PagedKVCache:
         if query.ndim != 3 or query.shape[2] != self.head_dim:
             raise ValueError(f"query must be [batch, heads, {self.head_dim}], got "
                              f"{query.shape}")
-        lens = [self.lens[b] for b in block_table]  # KeyError for unknown blocks
-        n = len(block_table)
+        pieces = [p for b in block_table for p in self._pieces(b)]  # KeyError for unknown
         B, H, D = query.shape
-        if n == 0:
+        if not pieces:
             return np.zeros(query.shape, dtype=np.float32)
+        n = len(pieces)
         dev = torch.device("cuda")
         qp = np.zeros((B, H, self._dp), dtype=np.float32)
         qp[..., :D] = query
         q_t = torch.from_numpy(qp).to(dev)
-        table = torch.tensor(block_table, dtype=torch.int32, device=dev).view(1, n).expand(B, n)
-        lens_t = torch.tensor(lens, dtype=torch.int32, device=dev).view(1, n).expand(B, n)
-        nb, bs, dp = self.num_blocks, self.block_size, self._dp
+        table = torch.tensor([s for s, _ in pieces], dtype=torch.int32,
+                             device=dev).view(1, n).expand(B, n)
+        lens_t = torch.tensor([r for _, r in pieces], dtype=torch.int32,
+                              device=dev).view(1, n).expand(B, n)
+        nb, bs, dp = self._cap, self.block_size, self._dp
         out = load_binding().decode_paged(
             q_t, self._k.view(nb, 1, bs, dp // 2), self._v.view(nb, 1, bs, dp), self._s,
             self._z, table, None, lens_t, 1, n, 0)
@@ -145,7 +203,7 @@ class INT4PagedKVCache:
         slot = (self._k[0].numel() * self._k.element_size()
                 + self._v[0].numel() * self._v.element_size()
                 + 2 * self._s[0].numel() * self._s.element_size())
-        stored = n * slot
+        stored = sum(len(s) for s in self._slots.values()) * slot
         fp16_equiv = sum(r * self.head_dim * 2 * 2 for r in self.lens.values())
         return {
             "blocks": n,

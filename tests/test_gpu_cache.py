@@ -113,7 +113,59 @@ class TestINT4PagedKVCache:
         with pytest.raises(KeyError):
             cache.decode_attention(np.zeros((1, 1, 64), np.float32), [3])
 
-    def test_oversized_block_rejected(self):
+    def test_malformed_blocks_rejected_before_the_cache_changes(self):
         cache = _cache(4, 16, 64)
+        k = np.random.randn(20, 64).astype(np.float32)
+        cache.write_block(0, k, k)
         with pytest.raises(ValueError):
-            cache.write_block(0, np.zeros((17, 64), np.float32), np.zeros((17, 64), np.float32))
+            cache.write_block(0, np.zeros((17, 63), np.float32), np.zeros((17, 63), np.float32))
+        with pytest.raises(ValueError):
+            cache.write_block(0, np.zeros((0, 64), np.float32), np.zeros((0, 64), np.float32))
+        with pytest.raises(AssertionError):
+            cache.write_block(0, np.zeros((17, 64), np.float32), np.zeros((16, 64), np.float32))
+        assert cache.lens[0] == 20
+        np.testing.assert_array_equal(cache.k_scale[0], quantize_int4_ref(k)[1])
+
+    def test_blocks_of_any_size_and_id(self):
+        """The reference's dictionaries take any block id and any row count
+        (src/vllm_integration.py:48-56): blocks longer than block_size take
+        several pool slots (the pool grows past num_blocks), each with the
+        block's one scale group, and decode as one page of the reference."""
+        from oracle import pack_int4
+        rng = np.random.RandomState(9)
+        cache = _cache(4, 16, 64)
+        blocks = {}
+        for b, rows in [(0, 40), (1000, 16), (2, 100), (-3, 1), (5, 17)]:
+            k = rng.randn(rows, 64).astype(np.float32)
+            v = rng.randn(rows, 64).astype(np.float32)
+            cache.write_block(b, k, v)
+            blocks[b] = (k, v)
+        # Rewriting a block with another length frees or takes slots.
+        k = rng.randn(33, 64).astype(np.float32)
+        v = rng.randn(33, 64).astype(np.float32)
+        cache.write_block(2, k, v)
+        blocks[2] = (k, v)
+        cache.free_block(5)
+        del blocks[5]
+        assert cache.memory_stats()["blocks"] == 4
+        table = [2, 1000, -3, 0, 2]
+        query = rng.randn(2, 3, 64).astype(np.float32)
+        got = cache.decode_attention(query, table)
+        pages, vals, lens = [], [], []
+        for b in table:
+            k, v = blocks[b]
+            q_, s_, z_ = quantize_int4_ref(k)
+            pages.append((q_, s_, z_))
+            vals.append(v.astype(np.float16).astype(np.float32))
+            lens.append(len(k))
+            np.testing.assert_array_equal(cache.k_packed[b], pack_int4(q_))
+            np.testing.assert_array_equal(cache.k_scale[b], s_)
+            np.testing.assert_array_equal(cache.k_zp[b], z_)
+            np.testing.assert_array_equal(cache.v[b], v.astype(np.float16))
+        ref = online_softmax_ref(query, pages, vals, np.array(lens))[0]
+        f64 = f64_attention(query, [p[0] for p in pages], [p[1] for p in pages],
+                            [p[2] for p in pages], vals, lens)
+        assert np.abs(got - ref).max() < 1e-5
+        assert np.abs(got - f64).max() < 1e-5
+        with pytest.raises(KeyError):
+            cache.decode_attention(query, [5])
