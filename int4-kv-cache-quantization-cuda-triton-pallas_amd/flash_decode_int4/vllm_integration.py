@@ -196,20 +196,29 @@ class INT4PagedKVCache:
         return out[..., :D].cpu().numpy()
 
     def memory_stats(self) -> dict:
-        """Bytes held for the written blocks (their full pool slots) vs fp16 K+V."""
+        """The stored data against fp16 K+V, counted as the reference counts its
+        arrays (src/vllm_integration.py:80-102: packed key rows, fp16 value
+        rows, a scale and a zero-point per block), plus ``pool_mb``, what the
+        device pool holds for the written blocks (whole slots of block_size
+        rows at the padded head_dim)."""
         n = len(self.lens)
         if n == 0:
-            return {"blocks": 0, "stored_mb": 0.0, "fp16_equiv_mb": 0.0, "ratio": 0.0}
+            return {"blocks": 0, "stored_mb": 0.0, "fp16_equiv_mb": 0.0, "ratio": 0.0,
+                    "pool_mb": 0.0}
+        D = self.head_dim
+        rows = sum(self.lens.values())
+        stored = rows * ((D + 1) // 2) + rows * D * 2 + n * 2 * D * 4
+        fp16_equiv = rows * D * 2 * 2
         slot = (self._k[0].numel() * self._k.element_size()
                 + self._v[0].numel() * self._v.element_size()
                 + 2 * self._s[0].numel() * self._s.element_size())
-        stored = sum(len(s) for s in self._slots.values()) * slot
-        fp16_equiv = sum(r * self.head_dim * 2 * 2 for r in self.lens.values())
+        pool = sum(len(s) for s in self._slots.values()) * slot
         return {
             "blocks": n,
             "stored_mb": round(stored / 1048576, 3),
             "fp16_equiv_mb": round(fp16_equiv / 1048576, 3),
             "ratio": round(fp16_equiv / max(stored, 1), 2),
+            "pool_mb": round(pool / 1048576, 3),
         }
 
 

@@ -86,6 +86,26 @@ class TestINT4PagedKVCache:
         stats = cache.memory_stats()
         assert stats["ratio"] > 1.5, stats
 
+    def test_memory_stats_count_the_stored_arrays(self):
+        """As the reference counts them (src/vllm_integration.py:80-102): the
+        bytes of the packed key rows, scales, zero-points and fp16 value rows
+        that the mapping views return; the pool's whole slots separately."""
+        rng = np.random.RandomState(4)
+        cache = _cache(4, 32, 48)
+        for b, rows in [(0, 32), (3, 7), (9, 70)]:
+            k = rng.randn(rows, 48).astype(np.float32)
+            cache.write_block(b, k, k)
+        stats = cache.memory_stats()
+        stored = sum(cache.k_packed[b].nbytes + cache.k_scale[b].nbytes + cache.k_zp[b].nbytes
+                     + cache.v[b].nbytes for b in cache.k_packed)
+        fp16 = sum(cache.lens[b] * 48 * 2 * 2 for b in cache.lens)
+        assert stats["stored_mb"] == round(stored / 1048576, 3)
+        assert stats["fp16_equiv_mb"] == round(fp16 / 1048576, 3)
+        assert stats["ratio"] == round(fp16 / stored, 2)
+        # 1 + 1 + 3 slots of 32 rows at the padded head_dim 64
+        slot = 32 * 32 + 32 * 64 * 2 + 2 * 64 * 4
+        assert stats["pool_mb"] == round(5 * slot / 1048576, 3)
+
     def test_packed_storage_is_real(self):
         from oracle import pack_int4
         np.random.seed(7)
